@@ -1,0 +1,93 @@
+"""ctypes binding of libbf16x_hip.so (the C ABI declared in include/bf16x_hip.h).
+
+torch is imported first on purpose: torch ships its own HIP runtime
+(torch/lib/libamdhip64.so, soname libamdhip64.so.7).  Loading this library
+after it makes the dynamic linker resolve our libamdhip64.so.7 dependency to
+that same runtime, so torch's streams and device pointers are valid here.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see module docstring)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbf16x_hip.so")
+
+OK = 0
+EARG, ESHAPE, ESTREAM_LEN, ETABLE, ECAPACITY, ESUB, EDTYPE = -1, -2, -3, -4, -5, -6, -7
+BF16, F16, F32 = 0, 1, 2
+EXACT, SATURATED = 0, 1
+
+_c_i32, _c_i64, _c_u32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32
+_P = ctypes.c_void_p
+
+# name -> (restype, argtypes); every function of include/bf16x_hip.h
+PROTOTYPES = {
+    "bf16x_version": (ctypes.c_char_p, []),
+    "bf16x_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "bf16x_stream_words": (_c_i64, [_c_i64, _c_i32]),
+    "bf16x_plan_tiles": (_c_i64, [_c_i64, _c_i64]),
+    "bf16x_encode_host": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i32, _P, _P, _P, _P, _P, _P, _c_i64,
+                                         ctypes.POINTER(_c_i64), _c_i32]),
+    "bf16x_plan_host": (ctypes.c_int, [_P, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
+                                       _c_i64, _c_i64, _c_i32, _P, _P, _c_i64, ctypes.POINTER(_c_i64)]),
+    "bf16x_plan_from_csr": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _c_i64, _c_i64, _c_i64, _P, _P]),
+    "bf16x_decode": (ctypes.c_int, [_P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P,
+                                    _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
+    "bf16x_gemv": (ctypes.c_int, [_P, _c_i32, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P,
+                                  _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
+}
+
+_LIB = None
+
+
+class Bf16xError(RuntimeError):
+    """A non-zero status returned by the C ABI."""
+
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {status_string(status)} (status {status})")
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it was not built (there is no fallback)."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m bfloat16x_amd.build` "
+                               "(the BF16X engine has no CPU fallback)")
+        h = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in PROTOTYPES.items():
+            fn = getattr(h, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = h
+    return _LIB
+
+
+def status_string(status: int) -> str:
+    try:
+        return lib().bf16x_status_string(int(status)).decode()
+    except Exception:  # pragma: no cover - only when the library itself is missing
+        return "unknown"
+
+
+def check(status: int, what: str) -> None:
+    if status != OK:
+        raise Bf16xError(int(status), what)
+
+
+def ptr(t) -> int | None:
+    """Data pointer of a tensor (None stays None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device):
+    """Raw hipStream_t of torch's current stream on `device`."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def version() -> str:
+    return lib().bf16x_version().decode()

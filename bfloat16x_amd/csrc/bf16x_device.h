@@ -1,0 +1,163 @@
+// Device-side building blocks of the BF16X engine (gfx950 / CDNA4).
+//
+// The packed-dict format (opqk_linear.py:291-324) stores, for 32 consecutive
+// flat elements starting at element 32*a (an "atom"):
+//   sign  word a              (bit j = sign of element j)
+//   mant  words 7a .. 7a+6    (element j's 7 bits at stream bits 7j..7j+6)
+//   delta words 3a .. 3a+2    (element j's 3-bit code at bits 3j..3j+2)
+//   emax  bytes 2a, 2a+1      (shared exponent of elements 0-15 / 16-31)
+// because every stream is LSB-first and 32 | (element offset) at atom starts.
+// A lane that owns an atom therefore loads 1 + 7 + 3 dwords and one u16 with
+// no cross-lane dependence, and consecutive lanes read consecutive bytes of
+// every stream (dwordx4 + dwordx3 for the 28-byte mantissa run, dwordx3 for
+// the 12-byte code run): the loads coalesce without an LDS round trip.
+//
+// Decoding works on "pairs" (element j, element j+16) packed as two bf16 in
+// one 32-bit register (j in the low half).  The two halves of an atom sit
+// 112 bits (mantissa) / 48 bits (codes) / 16 bits (sign) apart, so one
+// 16-bit-lane transposition of the mantissa and code words puts both fields
+// of a pair at the same offset of the two 16-bit lanes: every field is then
+// extracted for two elements with one 32-bit shift, and the sign of both
+// with one shift of the sign word.  The consumer (v_dot2_f32_bf16, an MFMA
+// operand, or a store) uses the same (j, j+16) pairing on its other operand.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bf16x {
+
+typedef uint32_t u32x4a __attribute__((ext_vector_type(4))) __attribute__((aligned(4)));
+typedef uint32_t u32x3a __attribute__((ext_vector_type(3))) __attribute__((aligned(4)));
+typedef uint32_t u32x2a __attribute__((ext_vector_type(2))) __attribute__((aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// NOTE: never __builtin_bit_cast an ext-vector *element* (v.y, v[1]) with
+// this toolchain: it reads element 0.  Copy the element to a scalar first.
+
+struct Atom {
+  uint32_t s;       // sign word
+  uint32_t m[7];    // mantissa words
+  uint32_t d[3];    // 3-bit code words
+  uint32_t e;       // emax byte of half 0 | emax byte of half 1 << 8
+};
+
+__device__ __forceinline__ uint32_t alignbit(uint32_t hi, uint32_t lo, uint32_t sh) {
+  return __builtin_amdgcn_alignbit(hi, lo, sh);
+}
+__device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
+  return __builtin_amdgcn_perm(s0, s1, sel);
+}
+// (a & 0xFFFF) | (b & 0xFFFF0000): one v_bfi_b32
+__device__ __forceinline__ uint32_t lo_hi(uint32_t a, uint32_t b) {
+  return (a & 0xFFFFu) | (b & 0xFFFF0000u);
+}
+// per-16-bit-lane saturating a - b (v_pk_sub_u16 ... clamp)
+__device__ __forceinline__ uint32_t pk_sub_sat(uint32_t a, uint32_t b) {
+  u16x2 x, y;
+  __builtin_memcpy(&x, &a, 4);
+  __builtin_memcpy(&y, &b, 4);
+  u16x2 r = __builtin_elementwise_sub_sat(x, y);
+  uint32_t o;
+  __builtin_memcpy(&o, &r, 4);
+  return o;
+}
+
+// Load the atom with flat atom index `ga` (all streams dword-aligned).
+__device__ __forceinline__ Atom load_atom(const uint32_t* __restrict__ sign,
+                                          const uint32_t* __restrict__ mant,
+                                          const uint32_t* __restrict__ delta,
+                                          const uint16_t* __restrict__ emax2,
+                                          uint64_t ga) {
+  Atom t;
+  const uint32_t* mp = mant + 7 * ga;
+  const uint32_t* dp = delta + 3 * ga;
+  u32x4a m03 = *(const u32x4a*)mp;
+  u32x3a m46 = *(const u32x3a*)(mp + 4);
+  u32x3a d02 = *(const u32x3a*)dp;
+  t.s = sign[ga];
+  t.e = emax2[ga];
+  uint32_t a0 = m03.x, a1 = m03.y, a2 = m03.z, a3 = m03.w;
+  uint32_t a4 = m46.x, a5 = m46.y, a6 = m46.z;
+  t.m[0] = a0; t.m[1] = a1; t.m[2] = a2; t.m[3] = a3;
+  t.m[4] = a4; t.m[5] = a5; t.m[6] = a6;
+  uint32_t b0 = d02.x, b1 = d02.y, b2 = d02.z;
+  t.d[0] = b0; t.d[1] = b1; t.d[2] = b2;
+  return t;
+}
+
+// Decode an atom into 16 packed pairs: out[j] = bf16(elem j) | bf16(elem j+16) << 16.
+// SAT: the 3-bit code is used as the delta (code 7 -> exponent emax-7); the
+// exponent is clamped at 0 like the reference kernels (bf16x_triton_test.py:50).
+__device__ __forceinline__ void decode_pairs(const Atom& t, uint32_t out[16]) {
+  // 16-bit-lane transposition: lane lo = elements 0..15, lane hi = 16..31
+  uint32_t pm[7];
+  pm[0] = lo_hi(t.m[0], t.m[3]);
+  pm[1] = alignbit(t.m[4], t.m[0], 16);
+  pm[2] = lo_hi(t.m[1], t.m[4]);
+  pm[3] = alignbit(t.m[5], t.m[1], 16);
+  pm[4] = lo_hi(t.m[2], t.m[5]);
+  pm[5] = alignbit(t.m[6], t.m[2], 16);
+  pm[6] = lo_hi(t.m[3], t.m[6]);
+  uint32_t pd[3];
+  pd[0] = lo_hi(t.d[0], t.d[1]);
+  pd[1] = alignbit(t.d[2], t.d[0], 16);
+  pd[2] = lo_hi(t.d[1], t.d[2]);
+  // emax of each half at bits 7..14 of its 16-bit lane
+  const uint32_t E = ((t.e & 0xFFu) << 7) | ((t.e & 0xFF00u) << 15);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    // mantissa field at lane bit 7j
+    const int mk = (7 * j) >> 4, mo = (7 * j) & 15;
+    uint32_t mraw;
+    if (mo <= 9) {
+      mraw = pm[mk] >> mo;
+    } else {
+      // field straddles two 16-bit chunks: splice byte 1 of chunk k with
+      // byte 0 of chunk k+1 in each lane, then the field sits at mo-8
+      mraw = perm(pm[mk + 1], pm[mk], 0x06030401u) >> (mo - 8);
+    }
+    // code field at lane bit 3j, moved to bits 7..9 of each lane
+    const int dk = (3 * j) >> 4, dof = (3 * j) & 15;
+    uint32_t dsh;
+    if (dof <= 13) {
+      dsh = (dof <= 7) ? (pd[dk] << (7 - dof)) : (pd[dk] >> (dof - 7));
+    } else {
+      dsh = perm(pd[dk + 1], pd[dk], 0x06030401u) << (15 - dof);
+    }
+    dsh &= 0x03800380u;
+    const uint32_t ex = pk_sub_sat(E, dsh);                 // (emax - d) << 7 per lane
+    const uint32_t ssh = (j == 15) ? t.s : (t.s << (15 - j));
+    // v_bitop3 0xEA = (S0 & S1) | S2: mantissa bits into the exponent word,
+    // then the two sign bits (ex has zeros at both masks' positions)
+    uint32_t w = __builtin_amdgcn_bitop3_b32(mraw, 0x007F007Fu, ex, 0xEA);
+    w = __builtin_amdgcn_bitop3_b32(ssh, 0x80008000u, w, 0xEA);
+    out[j] = w;
+  }
+}
+
+// bf16 bits of a finite-or-not float, round to nearest even, NaN kept NaN.
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x0040u) & 0xFFFFu;
+  return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+__device__ __forceinline__ float bf16lo_to_f32(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16hi_to_f32(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+__device__ __forceinline__ float dot2_bf16(uint32_t w, uint32_t x, float acc) {
+  bf16x2_t a, b;
+  __builtin_memcpy(&a, &w, 4);
+  __builtin_memcpy(&b, &x, 4);
+  return __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace bf16x

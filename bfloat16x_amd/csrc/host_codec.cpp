@@ -1,0 +1,220 @@
+// Host-side C++ of the BF16X engine: the packed-dict encoder and the
+// overflow-plan builder.  No GPU work happens here.
+//
+// bf16x_encode_host   -> bf16x_quantize (opqk_linear.py:291-324), byte-identical
+//                        output including the element padding of
+//                        pack_bits_stream (opqk_linear.py:53-64).
+// bf16x_plan_host     -> the overflow preparation of Bf16xFused.__init__
+//                        (bf16x_fused.py:165-182), re-encoded as per-tile
+//                        CSR offsets + 4-byte entries (column, exact bits).
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "../../include/bf16x_hip.h"
+
+namespace {
+
+constexpr int64_t kTileCols = 65536;
+
+int64_t words_of(int64_t n, int32_t b) {
+  const int64_t pad = ((-n * b) % 32 + 32) % 32;  // elements appended by the packer
+  const int64_t nbits = (n + pad) * b;
+  return (nbits + 31) / 32;
+}
+
+int host_threads(int32_t req) {
+  if (req > 0) return req;
+  unsigned hc = std::thread::hardware_concurrency();
+  return hc ? (int)std::min<unsigned>(hc, 64) : 4;
+}
+
+template <class F>
+void parallel_for(int64_t n_items, int nthreads, F&& f) {
+  if (n_items <= 0) return;
+  nthreads = (int)std::min<int64_t>(nthreads, n_items);
+  if (nthreads <= 1) {
+    f(0, n_items);
+    return;
+  }
+  std::vector<std::thread> th;
+  th.reserve(nthreads);
+  const int64_t per = (n_items + nthreads - 1) / nthreads;
+  for (int t = 0; t < nthreads; ++t) {
+    const int64_t b = t * per, e = std::min(n_items, b + per);
+    if (b >= e) break;
+    th.emplace_back([&f, b, e] { f(b, e); });
+  }
+  for (auto& x : th) x.join();
+}
+
+// Bit writer into a word array that stops at `limit` words.
+struct BitSink {
+  uint32_t* w;
+  int64_t limit;
+  void put(int64_t bitpos, uint32_t v, int nbits) {
+    const int64_t wi = bitpos >> 5;
+    const int sh = (int)(bitpos & 31);
+    const uint64_t x = (uint64_t)v << sh;
+    if (wi < limit) w[wi] |= (uint32_t)x;
+    if (sh + nbits > 32 && wi + 1 < limit) w[wi + 1] |= (uint32_t)(x >> 32);
+  }
+};
+
+}  // namespace
+
+extern "C" int64_t bf16x_stream_words(int64_t n, int32_t bits) {
+  if (n < 0 || bits <= 0 || bits > 32) return -1;
+  return words_of(n, bits);
+}
+
+extern "C" int64_t bf16x_plan_tiles(int64_t out_f, int64_t in_f) {
+  if (out_f <= 0 || in_f <= 0) return -1;
+  return out_f * ((in_f + kTileCols - 1) / kTileCols);
+}
+
+extern "C" int bf16x_encode_host(const uint16_t* w_bits, int64_t out_f, int64_t in_f, int32_t sub,
+                                 int32_t* sign, int32_t* mant, int32_t* delta, uint8_t* emax,
+                                 int32_t* ovf_idx, uint8_t* ovf_val, int64_t ovf_cap, int64_t* n_ovf,
+                                 int32_t n_threads) {
+  if (!w_bits || !sign || !mant || !delta || !emax || !n_ovf) return BF16X_EARG;
+  if (out_f <= 0 || in_f <= 0 || sub <= 0 || sub > 4096) return BF16X_ESHAPE;
+  if (ovf_cap < 0 || (ovf_cap > 0 && (!ovf_idx || !ovf_val))) return BF16X_EARG;
+  const int64_t N = out_f * in_f;
+  if (N > (int64_t)INT32_MAX) return BF16X_ESHAPE;  // the table stores int32 positions
+  const int64_t ws = words_of(N, 1), wm = words_of(N, 7), wd = words_of(N, 3);
+  memset(sign, 0, ws * 4);
+  memset(mant, 0, wm * 4);
+  memset(delta, 0, wd * 4);
+  const int64_t nsub = (N + sub - 1) / sub;
+
+  // work unit: a run of elements that starts on a 32-element and a sub-run
+  // boundary, so streams, emax and table counts split cleanly between threads
+  const int64_t unit = 32 * (int64_t)sub;
+  const int64_t n_units = (N + unit - 1) / unit;
+  const int nth = host_threads(n_threads);
+  std::vector<int64_t> cnt(n_units + 1, 0);
+
+  auto expo_at = [&](int64_t i) -> int32_t { return (w_bits[i] >> 7) & 0xFF; };
+
+  parallel_for(n_units, nth, [&](int64_t ub, int64_t ue) {
+    BitSink ss{(uint32_t*)sign, ws}, sm{(uint32_t*)mant, wm}, sd{(uint32_t*)delta, wd};
+    for (int64_t u = ub; u < ue; ++u) {
+      const int64_t e0 = u * unit, e1 = std::min(N, e0 + unit);
+      int64_t c = 0;
+      for (int64_t s0 = e0; s0 < e1; s0 += sub) {
+        const int64_t s1 = std::min(N, s0 + sub);
+        int32_t em = 0;  // tail of the last run is padded with e = 0
+        for (int64_t i = s0; i < s1; ++i) em = std::max(em, expo_at(i));
+        emax[s0 / sub] = (uint8_t)em;
+        for (int64_t i = s0; i < s1; ++i) {
+          const uint32_t b = w_bits[i];
+          const int32_t d = em - (int32_t)((b >> 7) & 0xFF);
+          if (d >= 7) ++c;
+          ss.put(i, (b >> 15) & 1u, 1);
+          sm.put(i * 7, b & 0x7Fu, 7);
+          sd.put(i * 3, (uint32_t)std::min(d, 7), 3);
+        }
+      }
+      cnt[u + 1] = c;
+    }
+  });
+  (void)nsub;
+  for (int64_t u = 0; u < n_units; ++u) cnt[u + 1] += cnt[u];
+  const int64_t total = cnt[n_units];
+  *n_ovf = total;
+  if (total > ovf_cap) return BF16X_ECAPACITY;
+  parallel_for(n_units, nth, [&](int64_t ub, int64_t ue) {
+    for (int64_t u = ub; u < ue; ++u) {
+      int64_t o = cnt[u];
+      const int64_t e0 = u * unit, e1 = std::min(N, e0 + unit);
+      for (int64_t i = e0; i < e1; ++i) {
+        const int32_t d = (int32_t)emax[i / sub] - expo_at(i);
+        if (d >= 7) {
+          ovf_idx[o] = (int32_t)i;
+          ovf_val[o] = (uint8_t)d;
+          ++o;
+        }
+      }
+    }
+  });
+  return BF16X_OK;
+}
+
+namespace {
+inline uint32_t get_bits(const int32_t* words, int64_t nwords, int64_t bit, int nb) {
+  const int64_t wi = bit >> 5;
+  const int sh = (int)(bit & 31);
+  uint64_t v = (uint32_t)words[wi];
+  if (sh + nb > 32 && wi + 1 < nwords) v |= (uint64_t)(uint32_t)words[wi + 1] << 32;
+  return (uint32_t)(v >> sh) & ((1u << nb) - 1u);
+}
+}  // namespace
+
+extern "C" int bf16x_plan_host(const int32_t* ovf_idx, const uint8_t* ovf_val, int64_t n_ovf,
+                               const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                               const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                               int64_t out_f, int64_t in_f, int32_t check,
+                               uint32_t* tile_off, uint32_t* tile_ent, int64_t ent_cap, int64_t* n_fix) {
+  if (!sign || !mant || !emax || !tile_off || !n_fix) return BF16X_EARG;
+  if (n_ovf < 0 || (n_ovf > 0 && (!ovf_idx || !ovf_val))) return BF16X_EARG;
+  if (check && !delta) return BF16X_EARG;
+  if (out_f <= 0 || in_f <= 0) return BF16X_ESHAPE;
+  const int64_t N = out_f * in_f;
+  if (n_sign < words_of(N, 1) || n_mant < words_of(N, 7) || n_emax < (N + 15) / 16 ||
+      (check && n_delta < words_of(N, 3)))
+    return BF16X_ESTREAM_LEN;
+  const int64_t tpr = (in_f + kTileCols - 1) / kTileCols;
+  const int64_t n_tiles = out_f * tpr;
+  memset(tile_off, 0, (n_tiles + 1) * sizeof(uint32_t));
+  // pass 1: validate and count entries per tile (kept entries: true delta > 7)
+  int64_t kept = 0, prev = -1;
+  for (int64_t j = 0; j < n_ovf; ++j) {
+    const int64_t p = ovf_idx[j];
+    const int v = ovf_val[j];
+    if (check) {
+      if (p <= prev || p < 0 || p >= N || v < 7) return BF16X_ETABLE;
+      if (get_bits(delta, n_delta, p * 3, 3) != 7u) return BF16X_ETABLE;
+      if (v > emax[p / 16]) return BF16X_ETABLE;
+      prev = p;
+    } else if (p < 0 || p >= N) {
+      return BF16X_ETABLE;  // never index out of range, even unchecked
+    }
+    if (v > 7) {
+      const int64_t row = p / in_f, col = p % in_f;
+      tile_off[row * tpr + col / kTileCols + 1] += 1;
+      ++kept;
+    }
+  }
+  if (check >= 2) {
+    // every code-7 element must be listed (full scan)
+    int64_t j = 0;
+    for (int64_t i = 0; i < N; ++i) {
+      if (get_bits(delta, n_delta, i * 3, 3) == 7u) {
+        while (j < n_ovf && ovf_idx[j] < i) ++j;
+        if (j >= n_ovf || ovf_idx[j] != i) return BF16X_ETABLE;
+      }
+    }
+  }
+  *n_fix = kept;
+  if (kept > (int64_t)UINT32_MAX) return BF16X_ESHAPE;
+  for (int64_t t = 0; t < n_tiles; ++t) tile_off[t + 1] += tile_off[t];
+  if (kept > ent_cap) return BF16X_ECAPACITY;
+  if (kept > 0 && !tile_ent) return BF16X_EARG;
+  // pass 2: entries in table order (ascending position = tile order, then column)
+  int64_t o = 0;
+  for (int64_t j = 0; j < n_ovf; ++j) {
+    const int v = ovf_val[j];
+    if (v <= 7) continue;
+    const int64_t p = ovf_idx[j];
+    const int64_t col = (p % in_f) % kTileCols;
+    const uint32_t s = get_bits(sign, n_sign, p, 1);
+    const uint32_t m = get_bits(mant, n_mant, p * 7, 7);
+    const uint32_t e = (uint32_t)((int)emax[p / 16] - v) & 0xFFu;  // opqk_linear.py:375
+    tile_ent[o++] = ((uint32_t)col << 16) | (s << 15) | (e << 7) | m;
+  }
+  return BF16X_OK;
+}

@@ -1,0 +1,151 @@
+"""Operator wrappers mirroring the reference's call surface.
+
+bf16x_decode / bf16x_decode_triton  <- bf16x_triton_test.py:80-108
+bf16x_fused_gemv                    <- bf16x_fused.py:114-127
+
+Every wrapper validates its tensors on the host, then calls one C-ABI entry
+point of libbf16x_hip.so on torch's current stream.  There is no fallback:
+a missing library or a CPU tensor raises.
+"""
+from __future__ import annotations
+
+import collections
+
+import torch
+
+from . import _lib
+from .codec import Bf16xPlan, build_plan_device, build_plan_from_csr, build_plan_host
+
+_X_DTYPES = {torch.bfloat16: _lib.BF16, torch.float16: _lib.F16, torch.float32: _lib.F32}
+
+
+def _dev_tensor(t: torch.Tensor, name: str, dtypes) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (the BF16X engine has no CPU path)")
+    if t.dtype not in dtypes:
+        raise TypeError(f"{name}: dtype {t.dtype} not in {dtypes}")
+    return t.contiguous()
+
+
+def _streams(sign, mant, delta, emax):
+    s = _dev_tensor(sign, "sign", (torch.int32,))
+    m = _dev_tensor(mant, "mant", (torch.int32,))
+    d = _dev_tensor(delta, "delta", (torch.int32,))
+    e = _dev_tensor(emax, "emax", (torch.uint8,))
+    dev = s.device
+    for t, nm in ((m, "mant"), (d, "delta"), (e, "emax")):
+        if t.device != dev:
+            raise ValueError(f"{nm} is on {t.device}, sign on {dev}")
+    return s, m, d, e
+
+
+class _PlanCache:
+    """Plans keyed by the identity and version of the tensors they came from.
+    Entries hold references to those tensors, so a key cannot be reused by a
+    different allocation while cached."""
+
+    def __init__(self, cap: int = 64):
+        self.cap = cap
+        self.d: "collections.OrderedDict" = collections.OrderedDict()
+
+    @staticmethod
+    def _key(ts, extra):
+        return tuple((t.data_ptr(), t.numel(), t._version, str(t.device)) for t in ts) + tuple(extra)
+
+    def get(self, ts, extra, make):
+        k = self._key(ts, extra)
+        hit = self.d.get(k)
+        if hit is not None:
+            self.d.move_to_end(k)
+            return hit[0]
+        plan = make()
+        self.d[k] = (plan, tuple(ts))
+        if len(self.d) > self.cap:
+            self.d.popitem(last=False)
+        return plan
+
+
+_PLANS = _PlanCache()
+
+
+def plan_for_table(sign, mant, emax, ovf_idx, ovf_val, out_f, in_f) -> Bf16xPlan:
+    """Device plan for a dict table given as (ovf_idx, ovf_val), cached."""
+    def make():
+        if in_f <= 65536:
+            return build_plan_device(ovf_idx, ovf_val, sign, mant, emax, out_f, in_f)
+        packed = dict(sign_packed=sign, mant_packed=mant, emax=emax, delta_ovf_idx=ovf_idx,
+                      delta_ovf_val=ovf_val, out_f=out_f, in_f=in_f, sub=16,
+                      delta_packed=torch.zeros(0, dtype=torch.int32))
+        return build_plan_host(packed, check=0, device=sign.device)
+    return _PLANS.get((sign, mant, emax, ovf_idx, ovf_val), (out_f, in_f), make)
+
+
+def plan_for_csr(olk, old, oloff, sign, mant, emax, out_f, in_f) -> Bf16xPlan:
+    return _PLANS.get((olk, old, oloff, sign, mant, emax), (out_f, in_f, "csr"),
+                      lambda: build_plan_from_csr(olk, old, oloff, sign, mant, emax, out_f, in_f))
+
+
+def bf16x_decode(sign, mant, delta, emax, out_f, in_f, ovf_idx=None, ovf_val=None, sub=16, *,
+                 plan: Bf16xPlan | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Decode a packed dict to bf16 [out_f, in_f] on the streams' GPU.
+
+    Same signature as bf16x_decode_triton (bf16x_triton_test.py:80): without a
+    table (ovf_idx/ovf_val None) the 3-bit codes are used as-is (the base
+    decode); with a table (or `plan`) the decode is exact.  Unlike the
+    reference, the table is turned into a device plan once and cached, so a
+    repeated call performs no host sync and no copy."""
+    s, m, d, e = _streams(sign, mant, delta, emax)
+    out_f, in_f = int(out_f), int(in_f)
+    if plan is None and ovf_idx is not None and ovf_val is not None and ovf_val.numel() > 0:
+        plan = plan_for_table(s, m, e, ovf_idx, ovf_val, out_f, in_f)
+    mode = _lib.SATURATED if plan is None else _lib.EXACT
+    if out is None:
+        out = torch.empty(out_f, in_f, dtype=torch.bfloat16, device=s.device)
+    elif out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() != out_f * in_f:
+        raise ValueError("out must be a contiguous bf16 tensor of out_f*in_f elements")
+    st = _lib.lib().bf16x_decode(s.data_ptr(), s.numel(), m.data_ptr(), m.numel(), d.data_ptr(), d.numel(),
+                                 e.data_ptr(), e.numel(), _lib.ptr(plan.tile_off) if plan else None,
+                                 _lib.ptr(plan.tile_ent) if plan else None, out_f, in_f, int(sub), mode,
+                                 out.data_ptr(), _lib.stream_of(s.device))
+    _lib.check(st, "bf16x_decode")
+    return out
+
+
+bf16x_decode_triton = bf16x_decode  # name of the reference entry point
+
+
+def bf16x_gemv(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None = None, sub=16,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """y[out_f] (bf16) = W . x with W decoded on the fly; exact with a plan,
+    saturated without one."""
+    s, m, d, e = _streams(sign, mant, delta, emax)
+    xx = _dev_tensor(x, "x", tuple(_X_DTYPES)).reshape(-1)
+    out_f, in_f = int(out_f), int(in_f)
+    if xx.numel() != in_f:
+        raise ValueError(f"x has {xx.numel()} elements, in_f = {in_f}")
+    y = out if out is not None else torch.empty(out_f, dtype=torch.bfloat16, device=s.device)
+    mode = _lib.SATURATED if plan is None else _lib.EXACT
+    st = _lib.lib().bf16x_gemv(xx.data_ptr(), _X_DTYPES[xx.dtype], s.data_ptr(), s.numel(), m.data_ptr(),
+                               m.numel(), d.data_ptr(), d.numel(), e.data_ptr(), e.numel(),
+                               _lib.ptr(plan.tile_off) if plan else None, _lib.ptr(plan.tile_ent) if plan else None,
+                               out_f, in_f, int(sub), mode, y.data_ptr(), _lib.stream_of(s.device))
+    _lib.check(st, "bf16x_gemv")
+    return y
+
+
+def bf16x_fused_gemv(x, sign, mant, delta, emax, olk, old, oloff, out_f, in_f, group=16, r=4, bk=256,
+                     num_warps=2, *, plan: Bf16xPlan | None = None) -> torch.Tensor:
+    """Fused decode+GEMV with the reference's signature (bf16x_fused.py:114).
+
+    olk/old/oloff is the reference's per-row CSR of entries with true delta
+    > 7; it is converted once (cached) into a plan.  `r`, `bk`, `num_warps`
+    are Triton tuning knobs with no meaning here and are ignored; `group`
+    must be 16."""
+    if group != 16:
+        raise _lib.Bf16xError(_lib.ESUB, "bf16x_fused_gemv")
+    if plan is None and oloff is not None:
+        s, m, _, e = _streams(sign, mant, delta, emax)
+        plan = plan_for_csr(olk, old, _dev_tensor(oloff, "oloff", (torch.int32,)), s, m, e, out_f, in_f)
+    return bf16x_gemv(x, sign, mant, delta, emax, out_f, in_f, plan=plan)

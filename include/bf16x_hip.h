@@ -1,0 +1,146 @@
+/*
+ * bf16x_hip.h -- C ABI of the MI355X (gfx950) BF16X engine (libbf16x_hip.so).
+ *
+ * The reference repository (dfytensor/bfloat16x) has no C ABI: its operator
+ * API is a set of Python functions that launch Triton kernels on the current
+ * torch stream.  Each entry point below replaces one of those functions (or a
+ * step inside one); the replaced interface is cited as file:line of the
+ * reference.  A Python/ctypes binding that mirrors the reference's call
+ * surface lives in bfloat16x_amd/.
+ *
+ * Conventions
+ *  - Plain pointers and sizes.  "dev" pointers are HIP device memory,
+ *    "host" pointers are ordinary host memory.  No entry point allocates
+ *    device memory; device outputs and workspaces are caller-owned.
+ *  - Packed-dict streams (the layout of bf16x_quantize, opqk_linear.py:291-324):
+ *      sign  int32 words, bit i = sign of flat element i (LSB-first)
+ *      mant  int32 words, 7 bits per element, LSB-first global bit stream
+ *      delta int32 words, 3 bits per element (code min(delta, 7))
+ *      emax  uint8, one per 16 consecutive flat elements
+ *    Stream lengths are given in words/bytes so the library can check them;
+ *    streams padded with extra words (the reference's _pad1) are accepted.
+ *  - Overflow plan: the sparse table entries whose true delta exceeds 7,
+ *    grouped per tile (tile = one row, or one 65536-column segment of a row
+ *    when in_f > 65536):
+ *      tile_off uint32 [n_tiles + 1]  CSR offsets into tile_ent
+ *      tile_ent uint32 [n_fix]        (column within tile << 16) | exact bf16 bits
+ *    Built by bf16x_plan_host() or bf16x_plan_from_csr().
+ *  - All device work is enqueued on `stream` (a hipStream_t; NULL = the
+ *    default stream) and is asynchronous.
+ *  - Return value: 0 = success, < 0 = invalid argument (see BF16X_E*),
+ *    > 0 = a hipError_t reported by the runtime.
+ *  - Entry points are stateless and reentrant.
+ */
+#ifndef BF16X_HIP_H
+#define BF16X_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* bf16x_stream_t; /* hipStream_t */
+
+enum {
+  BF16X_OK = 0,
+  BF16X_EARG = -1,         /* null pointer / bad enum / negative size        */
+  BF16X_ESHAPE = -2,       /* unsupported or inconsistent shape              */
+  BF16X_ESTREAM_LEN = -3,  /* a stream is shorter than the shape requires    */
+  BF16X_ETABLE = -4,       /* malformed overflow table                        */
+  BF16X_ECAPACITY = -5,    /* output capacity too small (count reported)      */
+  BF16X_ESUB = -6,         /* sub != 16 is not supported by the GPU kernels   */
+  BF16X_EDTYPE = -7        /* unsupported dtype code                          */
+};
+
+/* dtype codes for activations / outputs */
+enum { BF16X_BF16 = 0, BF16X_F16 = 1, BF16X_F32 = 2 };
+
+/* decode / GEMM weight semantics */
+enum {
+  BF16X_EXACT = 0,     /* lossless: table deltas applied (needs a plan)                   */
+  BF16X_SATURATED = 1  /* code 7 -> exponent emax-7, no table (bf16x_gemm_fused.py:84-87) */
+};
+
+/* Library version string, e.g. "bf16x-hip 0.1.0 gfx950". */
+const char* bf16x_version(void);
+/* Human-readable text for a status code. */
+const char* bf16x_status_string(int status);
+
+/* Words of pack_bits_stream(n values, bits) -- opqk_linear.py:53-64: the
+ * packer pads (-n*bits) % 32 *elements* before packing. */
+int64_t bf16x_stream_words(int64_t n, int32_t bits);
+
+/* ------------------------------------------------------------------------
+ * Host encoder.  Replaces bf16x_quantize(w, sub) (opqk_linear.py:291-324),
+ * byte-identical output.  w_bits: host bf16 bit patterns [out_f * in_f].
+ * Outputs (host): sign/mant/delta of bf16x_stream_words(N, 1/7/3) words,
+ * emax of ceil(N/sub) bytes, table of up to ovf_cap entries.  *n_ovf always
+ * receives the table size; BF16X_ECAPACITY if it exceeds ovf_cap (streams
+ * and emax are complete in that case).  n_threads <= 0: all host cores.
+ * ------------------------------------------------------------------------ */
+int bf16x_encode_host(const uint16_t* w_bits, int64_t out_f, int64_t in_f, int32_t sub,
+                      int32_t* sign, int32_t* mant, int32_t* delta, uint8_t* emax,
+                      int32_t* ovf_idx, uint8_t* ovf_val, int64_t ovf_cap, int64_t* n_ovf,
+                      int32_t n_threads);
+
+/* ------------------------------------------------------------------------
+ * Host plan builder.  Replaces the overflow preparation of Bf16xFused.__init__
+ * (bf16x_fused.py:165-182: keep val > 7, per-row CSR) with tile offsets and
+ * 4-byte entries carrying the exact bf16 bits.  Inputs are the host dict.
+ * check: 0 = trust the table, 1 = also verify order/range/val >= 7 and that
+ * each listed element carries code 7 (BF16X_ETABLE otherwise).
+ * tile_off: host [out_f * tiles_per_row + 1]; tile_ent: host, capacity ent_cap.
+ * *n_fix receives the entry count (BF16X_ECAPACITY if > ent_cap).
+ * ------------------------------------------------------------------------ */
+int64_t bf16x_plan_tiles(int64_t out_f, int64_t in_f);
+int bf16x_plan_host(const int32_t* ovf_idx, const uint8_t* ovf_val, int64_t n_ovf,
+                    const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                    const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                    int64_t out_f, int64_t in_f, int32_t check,
+                    uint32_t* tile_off, uint32_t* tile_ent, int64_t ent_cap, int64_t* n_fix);
+
+/* ------------------------------------------------------------------------
+ * Device plan from the reference's per-row CSR (olk col int32, old true
+ * delta int32, oloff int32 [out_f + 1]) -- the arguments of
+ * bf16x_fused_gemv (bf16x_fused.py:114) built at bf16x_fused.py:165-179.
+ * Writes tile_ent (dev, oloff[out_f] entries); tile_off is oloff itself
+ * (requires in_f <= 65536).  All pointers dev.
+ * ------------------------------------------------------------------------ */
+int bf16x_plan_from_csr(const int32_t* olk, const int32_t* old, const int32_t* oloff,
+                        const int32_t* sign, const int32_t* mant, const uint8_t* emax,
+                        int64_t out_f, int64_t in_f, int64_t n_entries,
+                        uint32_t* tile_ent, bf16x_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * One-pass decode.  Replaces bf16x_decode_triton (bf16x_triton_test.py:80-108)
+ * = _bf16x_decode_kernel (:11-52) + _bf16x_fix_ovf_kernel (:55-77): the
+ * table fix is applied in the same launch from the per-tile plan.
+ * mode BF16X_EXACT needs tile_off/tile_ent; BF16X_SATURATED ignores them.
+ * out: dev bf16 [out_f * in_f].  All pointers dev.
+ * ------------------------------------------------------------------------ */
+int bf16x_decode(const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                 const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                 const uint32_t* tile_off, const uint32_t* tile_ent,
+                 int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
+                 uint16_t* out, bf16x_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused decode + GEMV, batch 1.  Replaces bf16x_fused_gemv
+ * (bf16x_fused.py:114-127) / _bf16x_gemv_fused_kernel (:32-111):
+ * y[n] = sum_k W[n,k] * x[k], fp32 accumulation, y stored as bf16.
+ * x: dev [in_f] of x_dtype.  mode EXACT applies the plan, SATURATED not.
+ * Requires in_f % 32 == 0.  All pointers dev.
+ * ------------------------------------------------------------------------ */
+int bf16x_gemv(const void* x, int32_t x_dtype,
+               const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+               const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+               const uint32_t* tile_off, const uint32_t* tile_ent,
+               int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
+               uint16_t* y, bf16x_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BF16X_HIP_H */
