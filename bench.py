@@ -1,0 +1,202 @@
+"""Benchmark of the BF16X hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+Workload (BASELINE.json metric, configuration 2's headline shape): fused
+decode+GEMV, batch 1, of a 14336x4096 BF16X weight (N(0,0.02), 1% of
+entries x30, seed 0; lossless side table applied).  A step is one GEMV
+launch; consecutive steps rotate over distinct copies of the compressed
+weight totalling more than twice the 256 MB Infinity Cache, so each launch
+streams its weight from HBM.  Inputs are resident in HBM before timing.
+
+value = algorithmic bytes per launch / mean launch time (HIP events on the
+launch stream), where algorithmic bytes =
+4*(|sign|+|mant|+|delta|) + |emax| + 5*n_fix + 2*in_f + 2*out_f.
+Printed as one JSON line; diagnostics go to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def bench_weight(out_f: int, in_f: int, seed: int = 0) -> torch.Tensor:
+    """Configuration weights: N(0, 0.02), 1 % of entries x30, bf16 (CPU generator)."""
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(out_f, in_f, generator=g) * 0.02
+    n = w.numel()
+    idx = torch.randperm(n, generator=g)[: n // 100]
+    w.view(-1)[idx] *= 30.0
+    return w.to(torch.bfloat16)
+
+
+def alg_bytes_gemv(d: dict, n_fix: int) -> int:
+    return (4 * (d["sign_packed"].numel() + d["mant_packed"].numel() + d["delta_packed"].numel())
+            + d["emax"].numel() + 5 * n_fix + 2 * d["in_f"] + 2 * d["out_f"])
+
+
+def time_launches(fn, n_launch: int, warmup: int, stream) -> float:
+    """Mean seconds per launch over n_launch back-to-back launches."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(n_launch):
+        fn(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / 1e3 / n_launch
+
+
+def cpu_baseline(d: dict, alg_bytes_full: int, rows: int) -> dict:
+    """The reference's CPU decode+matmul path (restated in oracle/cpu_path.py)
+    on the first `rows` rows, scaled to compressed GB/s."""
+    from oracle.cpu_path import CpuBf16xLinear
+    torch.set_num_threads(os.cpu_count() or 1)
+    lin = CpuBf16xLinear(d, tile=1024)
+    x = torch.randn(1, d["in_f"], generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+    lin.forward(x, rows=rows)  # warm-up
+    ts = []
+    for _ in range(3):
+        t = time.perf_counter()
+        lin.forward(x, rows=rows)
+        ts.append(time.perf_counter() - t)
+    ts.sort()
+    frac = rows / d["out_f"]
+    gbs = alg_bytes_full * frac / ts[1] / 1e9
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            cpu = next(l.split(":", 1)[1].strip() for l in f if l.startswith("model name"))
+    except Exception:
+        pass
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"first {rows} of {d['out_f']} rows (decode+matmul, batch 1, median of 3 after 1 warm-up)",
+            "seconds_per_sample": round(ts[1], 4), "cpu": cpu}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-rows", type=int, default=7168)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import bfloat16x_amd as bx
+    from bfloat16x_amd import _lib
+    from bfloat16x_amd.ops import _X_DTYPES
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    out_f, in_f = 14336, 4096
+    t = time.time()
+    w = bench_weight(out_f, in_f, seed=0)
+    d = bx.bf16x_quantize(w)
+    plan = bx.build_plan_host(d)
+    log(f"weights + encode {time.time() - t:.1f}s; n_ovf={d['delta_ovf_idx'].numel()} n_fix={plan.n_fix}")
+    abytes = alg_bytes_gemv(d, plan.n_fix)
+    comp_bytes = sum(d[k].numel() * d[k].element_size() for k in ("sign_packed", "mant_packed", "delta_packed",
+                                                                   "emax")) + plan.nbytes
+    n_copies = max(2, -(-3 * MALL_BYTES // comp_bytes))
+    copies = []
+    for _ in range(n_copies):
+        g = {k: d[k].to(dev) for k in ("sign_packed", "mant_packed", "delta_packed", "emax")}
+        p = plan.to(dev)
+        copies.append((g, p))
+    x = torch.randn(in_f, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+    y = torch.empty(out_f, dtype=torch.bfloat16, device=dev)
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+    sp = _lib.stream_of(dev)
+    argv = []
+    for g, p in copies:
+        argv.append((x.data_ptr(), _X_DTYPES[x.dtype], g["sign_packed"].data_ptr(), g["sign_packed"].numel(),
+                     g["mant_packed"].data_ptr(), g["mant_packed"].numel(), g["delta_packed"].data_ptr(),
+                     g["delta_packed"].numel(), g["emax"].data_ptr(), g["emax"].numel(), p.tile_off.data_ptr(),
+                     p.tile_ent.data_ptr(), p.tile_sat.data_ptr(), out_f, in_f, 16, _lib.EXACT, y.data_ptr(), sp))
+    # correctness guard on the benchmarked inputs (exact decode of copy 0 == weight)
+    wd = w.to(dev)
+    dec = bx.bf16x_decode(copies[0][0]["sign_packed"], copies[0][0]["mant_packed"], copies[0][0]["delta_packed"],
+                          copies[0][0]["emax"], out_f, in_f, plan=copies[0][1])
+    assert torch.equal(dec.view(torch.int16), wd.view(torch.int16)), "decode mismatch on benchmark weights"
+    del dec
+    st = lib.bf16x_gemv(*argv[0])
+    _lib.check(st, "bf16x_gemv")
+
+    def step(i):
+        lib.bf16x_gemv(*argv[i % n_copies])
+
+    sec = time_launches(step, args.steps, args.warmup, stream)
+    gbs = abytes / sec / 1e9
+    log(f"bf16x gemv: {sec * 1e6:.2f} us/launch, {gbs:.1f} GB/s algorithmic ({n_copies} rotating copies)")
+
+    # plain bf16 GEMV comparator (torch / hipBLASLt) with the same rotation
+    wcopies = [wd] + [wd.clone() for _ in range(max(1, -(-3 * MALL_BYTES // (wd.numel() * 2))) - 1)]
+    xb = x.view(1, in_f)
+
+    def step_bf16(i):
+        torch.nn.functional.linear(xb, wcopies[i % len(wcopies)])
+
+    sec_bf16 = time_launches(step_bf16, max(200, args.steps // 4), 20, stream)
+    log(f"bf16 F.linear gemv: {sec_bf16 * 1e6:.2f} us ({wd.numel() * 2 / sec_bf16 / 1e9:.1f} GB/s of bf16 bytes)")
+    del wcopies
+
+    cpu = None
+    if not args.no_cpu:
+        t = time.time()
+        cpu = cpu_baseline(d, abytes, args.cpu_rows)
+        log(f"cpu baseline {cpu} ({time.time() - t:.1f}s)")
+
+    rec = {
+        "metric": "decode+GEMV compressed GB/s (% HBM peak) @14336x4096; decode+GEMM TFLOP/s",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec * 1e3, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "bf16x fused decode+GEMV 14336x4096, batch 1, exact (side table applied)",
+                   "out_f": out_f, "in_f": in_f, "weights": "N(0,0.02), 1% x30, seed 0",
+                   "rotating_copies": n_copies, "alg_bytes_per_launch": abytes},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "bf16_gemv_us": round(sec_bf16 * 1e6, 3),
+        "speedup_vs_bf16_gemv": round(sec_bf16 / sec, 3),
+        "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 2),
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -32,11 +32,11 @@ PROTOTYPES = {
     "bf16x_encode_host": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i32, _P, _P, _P, _P, _P, _P, _c_i64,
                                          ctypes.POINTER(_c_i64), _c_i32]),
     "bf16x_plan_host": (ctypes.c_int, [_P, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
-                                       _c_i64, _c_i64, _c_i32, _P, _P, _c_i64, ctypes.POINTER(_c_i64)]),
-    "bf16x_plan_from_csr": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _c_i64, _c_i64, _c_i64, _P, _P]),
+                                       _c_i64, _c_i64, _c_i32, _P, _P, _P, _c_i64, ctypes.POINTER(_c_i64)]),
+    "bf16x_plan_from_csr": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _c_i64, _c_i64, _c_i64, _P, _P, _P]),
     "bf16x_decode": (ctypes.c_int, [_P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P,
                                     _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
-    "bf16x_gemv": (ctypes.c_int, [_P, _c_i32, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P,
+    "bf16x_gemv": (ctypes.c_int, [_P, _c_i32, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P, _P,
                                   _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
 }
 

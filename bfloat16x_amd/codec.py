@@ -71,19 +71,22 @@ def bf16x_quantize(w: torch.Tensor, sub: int = SUB, n_threads: int = 0) -> dict:
 
 @dataclass
 class Bf16xPlan:
-    """Device overflow plan: tile_off uint32 [n_tiles+1], tile_ent uint32 [n_fix]."""
+    """Device overflow plan: tile_off uint32 [n_tiles+1], tile_ent uint32 [n_fix]
+    ((column << 16) | exact bits), tile_sat uint8 [n_fix] (max(emax - 7, 0))."""
     tile_off: torch.Tensor
     tile_ent: torch.Tensor
+    tile_sat: torch.Tensor
     n_fix: int
     out_f: int
     in_f: int
 
     @property
     def nbytes(self) -> int:
-        return self.tile_off.numel() * 4 + self.tile_ent.numel() * 4
+        return self.tile_off.numel() * 4 + self.tile_ent.numel() * 4 + self.tile_sat.numel()
 
     def to(self, device) -> "Bf16xPlan":
-        return Bf16xPlan(self.tile_off.to(device), self.tile_ent.to(device), self.n_fix, self.out_f, self.in_f)
+        return Bf16xPlan(self.tile_off.to(device), self.tile_ent.to(device), self.tile_sat.to(device),
+                         self.n_fix, self.out_f, self.in_f)
 
 
 def plan_tiles(out_f: int, in_f: int) -> int:
@@ -112,14 +115,16 @@ def build_plan_host(packed: dict, check: int = 1, device=None) -> Bf16xPlan:
     tile_off = torch.empty(n_tiles + 1, dtype=torch.int32)
     cap = int((val > 7).sum())
     tile_ent = torch.empty(max(cap, 1), dtype=torch.int32)
+    tile_sat = torch.zeros(max(cap, 1), dtype=torch.uint8)
     n_fix = ctypes.c_int64(0)
     st = _lib.lib().bf16x_plan_host(idx.data_ptr(), val.data_ptr(), idx.numel(), sign.data_ptr(), sign.numel(),
                                     mant.data_ptr(), mant.numel(), delta.data_ptr(), delta.numel(),
                                     emax.data_ptr(), emax.numel(), out_f, in_f, int(check),
-                                    tile_off.data_ptr(), tile_ent.data_ptr(), cap, ctypes.byref(n_fix))
+                                    tile_off.data_ptr(), tile_ent.data_ptr(), tile_sat.data_ptr(), cap,
+                                    ctypes.byref(n_fix))
     _lib.check(st, "bf16x_plan_host")
     k = int(n_fix.value)
-    plan = Bf16xPlan(tile_off, tile_ent[:max(k, 1)].clone(), k, out_f, in_f)
+    plan = Bf16xPlan(tile_off, tile_ent[:max(k, 1)].clone(), tile_sat[:max(k, 1)].clone(), k, out_f, in_f)
     return plan.to(device) if device is not None else plan
 
 
@@ -128,12 +133,14 @@ def build_plan_from_csr(olk, old, oloff, sign, mant, emax, out_f: int, in_f: int
     offsets are reused as tile offsets, entries are re-encoded on the GPU."""
     dev = sign.device
     n = int(olk.numel())
-    ent = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    ent = torch.zeros(max(n, 1), dtype=torch.int32, device=dev)
+    sat = torch.zeros(max(n, 1), dtype=torch.uint8, device=dev)
     st = _lib.lib().bf16x_plan_from_csr(_lib.ptr(olk.contiguous()), _lib.ptr(old.contiguous()),
                                         oloff.data_ptr(), sign.data_ptr(), mant.data_ptr(), emax.data_ptr(),
-                                        int(out_f), int(in_f), n, ent.data_ptr(), _lib.stream_of(dev))
+                                        int(out_f), int(in_f), n, ent.data_ptr(), sat.data_ptr(),
+                                        _lib.stream_of(dev))
     _lib.check(st, "bf16x_plan_from_csr")
-    return Bf16xPlan(oloff.to(torch.int32), ent, n, int(out_f), int(in_f))
+    return Bf16xPlan(oloff.to(torch.int32), ent, sat, n, int(out_f), int(in_f))
 
 
 def build_plan_device(ovf_idx, ovf_val, sign, mant, emax, out_f: int, in_f: int) -> Bf16xPlan:

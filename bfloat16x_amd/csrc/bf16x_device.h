@@ -30,6 +30,7 @@ typedef uint32_t u32x4a __attribute__((ext_vector_type(4))) __attribute__((align
 typedef uint32_t u32x3a __attribute__((ext_vector_type(3))) __attribute__((aligned(4)));
 typedef uint32_t u32x2a __attribute__((ext_vector_type(2))) __attribute__((aligned(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 

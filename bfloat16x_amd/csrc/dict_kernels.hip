@@ -1,9 +1,7 @@
-// Packed-dict kernels for gfx950: one-pass decode, fused decode+GEMV, and
-// the device conversion of the reference's per-row CSR into a plan.
+// Packed-dict kernels for gfx950: one-pass decode and the device conversion of the reference's per-row CSR into a plan.
 //
 //   decode  <- _bf16x_decode_kernel + _bf16x_fix_ovf_kernel
 //              (bf16x_triton_test.py:11-77), fix folded into the same launch
-//   gemv    <- _bf16x_gemv_fused_kernel (bf16x_fused.py:32-111)
 //   csr     <- consumer of the CSR built at bf16x_fused.py:165-179
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -107,174 +105,12 @@ __global__ __launch_bounds__(256) void decode_elems_kernel(
 }
 
 // --------------------------------------------------------------------------
-// fused decode + GEMV (batch 1)
-//
-// Block = 4 waves; each wave owns whole rows.  x is staged once per block in
-// LDS in the decoder's (j, j+16) pairing: pair j of atom a = x[32a+j] (low
-// half) | x[32a+16+j] (high half).  The 16-byte chunks of an atom are
-// XOR-swizzled so that 8 lanes reading the same chunk of 8 consecutive atoms
-// hit 8 distinct 4-bank groups.  Lane l of a wave handles atoms l, l+64, ...
-// of its row, so the weight loads of a wave are contiguous in every stream.
-// The saturated weight is accumulated in the main loop; the plan entries of
-// the row then add (w_exact - w_sat) * x[k], the reference's correction
-// overlay (bf16x_fused.py:83-109).
-// --------------------------------------------------------------------------
-template <bool XF32>
-struct XStage;
-
-// bf16 activations: 16 u32 pairs per atom (4 chunks of 16 B)
-template <>
-struct XStage<false> {
-  static constexpr int kWordsPerAtom = 16;
-  __device__ static __forceinline__ int chunk_pos(int64_t a, int c) { return c ^ (int)((a >> 1) & 3); }
-  __device__ static void stage(const void* __restrict__ xv, int64_t P, uint32_t* xs) {
-    const uint16_t* xb = (const uint16_t*)xv;
-    for (int64_t h = threadIdx.x; h < 2 * P; h += blockDim.x) {
-      const int64_t a = h >> 1;
-      const int half = (int)(h & 1);
-      const u32x4a lv = *(const u32x4a*)(xb + 32 * a + 8 * half);
-      const u32x4a hv = *(const u32x4a*)(xb + 32 * a + 16 + 8 * half);
-      uint32_t l[4] = {lv.x, lv.y, lv.z, lv.w};
-      uint32_t hh[4] = {hv.x, hv.y, hv.z, hv.w};
-      uint32_t q[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        q[2 * i] = perm(hh[i], l[i], 0x05040100u);
-        q[2 * i + 1] = perm(hh[i], l[i], 0x07060302u);
-      }
-      u32x4* dst = (u32x4*)(xs + a * 16);
-      dst[chunk_pos(a, 2 * half)] = u32x4{q[0], q[1], q[2], q[3]};
-      dst[chunk_pos(a, 2 * half + 1)] = u32x4{q[4], q[5], q[6], q[7]};
-    }
-  }
-  __device__ static __forceinline__ void load(const uint32_t* xs, int64_t a, uint32_t xp[16]) {
-    const u32x4* src = (const u32x4*)(xs + a * 16);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const u32x4 v = src[chunk_pos(a, c)];
-      xp[4 * c + 0] = v.x; xp[4 * c + 1] = v.y; xp[4 * c + 2] = v.z; xp[4 * c + 3] = v.w;
-    }
-  }
-  __device__ static __forceinline__ float at(const uint32_t* xs, int64_t k) {
-    const int64_t a = k >> 5;
-    const int j = (int)(k & 15), hi = (int)((k >> 4) & 1);
-    const uint32_t w = xs[a * 16 + chunk_pos(a, j >> 2) * 4 + (j & 3)];
-    return hi ? bf16hi_to_f32(w) : bf16lo_to_f32(w);
-  }
-  __device__ static __forceinline__ void dot(const uint32_t w[16], const uint32_t xp[16], float& acc0,
-                                             float& acc1) {
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      acc0 = dot2_bf16(w[j], xp[j], acc0);
-      acc1 = dot2_bf16(w[j + 1], xp[j + 1], acc1);
-    }
-  }
-};
-
-// fp16 / fp32 activations, kept as fp32: 16 float pairs per atom (8 chunks)
-template <>
-struct XStage<true> {
-  static constexpr int kWordsPerAtom = 32;
-  __device__ static __forceinline__ int chunk_pos(int64_t a, int c) { return c ^ (int)(a & 7); }
-  int dummy;
-};
-
-template <int XT>
-__device__ __forceinline__ float load_x_elem(const void* xv, int64_t k) {
-  if (XT == BF16X_F32) return ((const float*)xv)[k];
-  return (float)((const _Float16*)xv)[k];
-}
-
-template <int XT>
-__device__ void stage_x_f32(const void* __restrict__ xv, int64_t P, uint32_t* xs) {
-  for (int64_t h = threadIdx.x; h < 16 * P; h += blockDim.x) {
-    const int64_t a = h >> 4;
-    const int j = (int)(h & 15);
-    const float lo = load_x_elem<XT>(xv, 32 * a + j);
-    const float hi = load_x_elem<XT>(xv, 32 * a + 16 + j);
-    const int c = j >> 1;
-    float* dst = (float*)(xs + a * 32 + XStage<true>::chunk_pos(a, c) * 4 + (j & 1) * 2);
-    dst[0] = lo;
-    dst[1] = hi;
-  }
-}
-
-template <int XT>
-__global__ __launch_bounds__(256) void gemv_kernel(
-    const void* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
-    const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
-    const uint32_t* __restrict__ tile_off, const uint32_t* __restrict__ tile_ent, int64_t out_f,
-    int64_t in_f, int tpr, int rows_per_wave, uint16_t* __restrict__ y) {
-  extern __shared__ uint32_t xs[];
-  constexpr bool XF = (XT != BF16X_BF16);
-  const int64_t P = in_f >> 5;
-  if (XF) stage_x_f32<XT>(x, P, xs);
-  else XStage<false>::stage(x, P, xs);
-  __syncthreads();
-
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t rows_per_block = 4 * (int64_t)rows_per_wave;
-  const uint8_t* emax = (const uint8_t*)emax2;
-  for (int i = 0; i < rows_per_wave; ++i) {
-    const int64_t row = (int64_t)blockIdx.x * rows_per_block + (int64_t)i * 4 + wave;
-    if (row >= out_f) break;
-    float acc0 = 0.f, acc1 = 0.f;
-    for (int64_t a = lane; a < P; a += 64) {
-      const Atom t = load_atom(sign, mant, delta, emax2, row * P + a);
-      uint32_t w[16];
-      decode_pairs(t, w);
-      if (!XF) {
-        uint32_t xp[16];
-        XStage<false>::load(xs, a, xp);
-        XStage<false>::dot(w, xp, acc0, acc1);
-      } else {
-        const u32x4* src = (const u32x4*)(xs + a * 32);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const u32x4 v = src[XStage<true>::chunk_pos(a, c)];
-          const uint32_t w0 = w[2 * c], w1 = w[2 * c + 1];
-          acc0 = fmaf(bf16lo_to_f32(w0), __uint_as_float(v.x), acc0);
-          acc1 = fmaf(bf16hi_to_f32(w0), __uint_as_float(v.y), acc1);
-          acc0 = fmaf(bf16lo_to_f32(w1), __uint_as_float(v.z), acc0);
-          acc1 = fmaf(bf16hi_to_f32(w1), __uint_as_float(v.w), acc1);
-        }
-      }
-    }
-    if (tile_off != nullptr) {
-      for (int seg = 0; seg < tpr; ++seg) {
-        const int64_t tt = row * tpr + seg;
-        const uint32_t e0 = tile_off[tt], e1 = tile_off[tt + 1];
-        for (uint32_t e = e0 + lane; e < e1; e += 64) {
-          const uint32_t ent = tile_ent[e];
-          const int64_t k = (int64_t)seg * kTileCols + (ent >> 16);
-          if (k >= in_f) continue;  // a bad plan never reads out of range
-          const uint32_t ex = ent & 0xFFFFu;
-          const int em = (int)emax[(row * in_f + k) >> 4];
-          const uint32_t sat = (ex & 0x807Fu) | ((uint32_t)max(em - 7, 0) << 7);
-          float xk;
-          if (XF) {
-            const int64_t a = k >> 5;
-            const int j = (int)(k & 15), hi = (int)((k >> 4) & 1);
-            xk = __uint_as_float(xs[a * 32 + XStage<true>::chunk_pos(a, j >> 1) * 4 + (j & 1) * 2 + hi]);
-          } else {
-            xk = XStage<false>::at(xs, k);
-          }
-          acc0 = fmaf(bf16lo_to_f32(ex) - bf16lo_to_f32(sat), xk, acc0);
-        }
-      }
-    }
-    const float tot = wave_sum(acc0 + acc1);
-    if (lane == 0) y[row] = (uint16_t)f32_to_bf16_rne(tot);
-  }
-}
-
-// --------------------------------------------------------------------------
 // reference CSR (col, true delta, row offsets) -> plan entries
 // --------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void plan_from_csr_kernel(
     const int32_t* __restrict__ olk, const int32_t* __restrict__ old, const int32_t* __restrict__ oloff,
     const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant, const uint8_t* __restrict__ emax,
-    int64_t out_f, int64_t in_f, int64_t n_entries, uint32_t* __restrict__ ent) {
+    int64_t out_f, int64_t in_f, int64_t n_entries, uint32_t* __restrict__ ent, uint8_t* __restrict__ sat) {
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= out_f) return;
   const int lane = threadIdx.x & 63;
@@ -285,8 +121,10 @@ __global__ __launch_bounds__(256) void plan_from_csr_kernel(
     const int64_t p = row * in_f + k;
     const uint32_t s = field_at(sign, p, 1);
     const uint32_t m = field_at(mant, p * 7, 7);
-    const int e = min(max((int)emax[p >> 4] - td, 0), 255);  // bf16x_fused.py:103
+    const int em = (int)emax[p >> 4];
+    const int e = min(max(em - td, 0), 255);  // bf16x_fused.py:103
     ent[j] = ((uint32_t)k << 16) | (s << 15) | ((uint32_t)e << 7) | m;
+    sat[j] = (uint8_t)max(em - 7, 0);
   }
 }
 
@@ -294,23 +132,6 @@ __global__ __launch_bounds__(256) void plan_from_csr_kernel(
 
 using namespace bf16x;
 
-namespace {
-
-int check_dict(int64_t out_f, int64_t in_f, int32_t sub, int64_t n_sign, int64_t n_mant, int64_t n_delta,
-               int64_t n_emax) {
-  if (out_f <= 0 || in_f <= 0) return BF16X_ESHAPE;
-  if (sub != 16) return BF16X_ESUB;
-  const int64_t N = out_f * in_f;
-  if (N > ((int64_t)1 << 36)) return BF16X_ESHAPE;
-  if (n_sign < bf16x_stream_words(N, 1) || n_mant < bf16x_stream_words(N, 7) ||
-      n_delta < bf16x_stream_words(N, 3) || n_emax < (N + 15) / 16)
-    return BF16X_ESTREAM_LEN;
-  return BF16X_OK;
-}
-
-int tiles_per_row(int64_t in_f) { return (int)((in_f + kTileCols - 1) / kTileCols); }
-
-}  // namespace
 
 extern "C" int bf16x_decode(const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
                             const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
@@ -346,50 +167,16 @@ extern "C" int bf16x_decode(const int32_t* sign, int64_t n_sign, const int32_t* 
   return launch_status();
 }
 
-extern "C" int bf16x_gemv(const void* x, int32_t x_dtype, const int32_t* sign, int64_t n_sign,
-                          const int32_t* mant, int64_t n_mant, const int32_t* delta, int64_t n_delta,
-                          const uint8_t* emax, int64_t n_emax, const uint32_t* tile_off,
-                          const uint32_t* tile_ent, int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
-                          uint16_t* y, bf16x_stream_t stream) {
-  if (!x || !sign || !mant || !delta || !emax || !y) return BF16X_EARG;
-  if (mode != BF16X_EXACT && mode != BF16X_SATURATED) return BF16X_EARG;
-  if (mode == BF16X_EXACT && (!tile_off || !tile_ent)) return BF16X_EARG;
-  if (x_dtype != BF16X_BF16 && x_dtype != BF16X_F16 && x_dtype != BF16X_F32) return BF16X_EDTYPE;
-  int rc = check_dict(out_f, in_f, sub, n_sign, n_mant, n_delta, n_emax);
-  if (rc) return rc;
-  if ((in_f & 31) != 0) return BF16X_ESHAPE;
-  if (!aligned4(sign) || !aligned4(mant) || !aligned4(delta) || !aligned2(emax)) return BF16X_EARG;
-  if (x_dtype == BF16X_BF16 && !aligned16(x)) return BF16X_EARG;
-  const size_t lds = (size_t)in_f * (x_dtype == BF16X_BF16 ? 2 : 4);
-  if (lds > 64 * 1024) return BF16X_ESHAPE;
-  const uint32_t* to = (mode == BF16X_EXACT) ? tile_off : nullptr;
-  const int tpr = tiles_per_row(in_f);
-  const int rpw = 1;
-  const int64_t grid = (out_f + 4 * rpw - 1) / (4 * rpw);
-  if (grid > INT32_MAX) return BF16X_ESHAPE;
-  hipStream_t st = (hipStream_t)stream;
-#define BF16X_GEMV_LAUNCH(XT)                                                                           \
-  hipLaunchKernelGGL(gemv_kernel<XT>, dim3((unsigned)grid), dim3(256), lds, st, x, (const uint32_t*)sign, \
-                     (const uint32_t*)mant, (const uint32_t*)delta, (const uint16_t*)emax, to, tile_ent,    \
-                     out_f, in_f, tpr, rpw, y)
-  switch (x_dtype) {
-    case BF16X_BF16: BF16X_GEMV_LAUNCH(BF16X_BF16); break;
-    case BF16X_F16: BF16X_GEMV_LAUNCH(BF16X_F16); break;
-    default: BF16X_GEMV_LAUNCH(BF16X_F32); break;
-  }
-#undef BF16X_GEMV_LAUNCH
-  return launch_status();
-}
-
 extern "C" int bf16x_plan_from_csr(const int32_t* olk, const int32_t* old, const int32_t* oloff,
                                    const int32_t* sign, const int32_t* mant, const uint8_t* emax, int64_t out_f,
-                                   int64_t in_f, int64_t n_entries, uint32_t* tile_ent, bf16x_stream_t stream) {
+                                   int64_t in_f, int64_t n_entries, uint32_t* tile_ent, uint8_t* tile_sat,
+                                   bf16x_stream_t stream) {
   if (!oloff || !sign || !mant || !emax) return BF16X_EARG;
-  if (n_entries < 0 || (n_entries > 0 && (!olk || !old || !tile_ent))) return BF16X_EARG;
+  if (n_entries < 0 || (n_entries > 0 && (!olk || !old || !tile_ent || !tile_sat))) return BF16X_EARG;
   if (out_f <= 0 || in_f <= 0 || in_f > kTileCols) return BF16X_ESHAPE;
   if (n_entries == 0) return BF16X_OK;
   const int64_t grid = (out_f + 3) / 4;
   hipLaunchKernelGGL(plan_from_csr_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, olk, old,
-                     oloff, (const uint32_t*)sign, (const uint32_t*)mant, emax, out_f, in_f, n_entries, tile_ent);
+                     oloff, (const uint32_t*)sign, (const uint32_t*)mant, emax, out_f, in_f, n_entries, tile_ent, tile_sat);
   return launch_status();
 }

@@ -1,0 +1,456 @@
+// Fused decode + GEMV (batch 1) on gfx950.
+//
+// Replaces _bf16x_gemv_fused_kernel / bf16x_fused_gemv (bf16x_fused.py:32-127):
+// y[n] = sum_k W[n,k] x[k], fp32 accumulation, y stored as bf16 (RNE).  The
+// main loop accumulates the saturated weight (code 7 -> exponent emax-7);
+// the plan entries of the row then add (w_exact - w_sat) * x[k], the
+// correction overlay of bf16x_fused.py:83-109.
+//
+// Work split.  A row's P = in_f/32 atoms are divided among G waves of a
+// 4-wave workgroup (G = 1, 2, 4); lane l of part g owns atoms
+// g*ceil(P/G) + 64*s + l, s < NS, of EVERY row the workgroup visits.  The
+// x values of those atoms are therefore loaded once per wave, kept in VGPRs
+// in the decoder's (j, j+16) pairing, and no LDS is needed for x.  A
+// workgroup visits `iters` groups of 4/G rows; each wave software-pipelines
+// its rows: while row r is decoded and reduced, the atoms and the plan
+// entries of row r+4/G are already in flight, and the (emax, x[k]) gathers
+// of row r's entries were issued before that prefetch so that waiting for
+// them never waits for the prefetch (vector loads complete in issue order).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "../../include/bf16x_hip.h"
+#include "bf16x_device.h"
+#include "launch_common.h"
+
+namespace bf16x {
+
+template <int XT>
+__device__ __forceinline__ float load_x_elem(const void* __restrict__ x, int64_t k) {
+  if constexpr (XT == BF16X_BF16) return __uint_as_float((uint32_t)((const uint16_t*)x)[k] << 16);
+  else if constexpr (XT == BF16X_F32) return ((const float*)x)[k];
+  else return (float)((const _Float16*)x)[k];
+}
+
+// x values of atom a from global memory in pair order: bf16 -> 16 words
+// (x[32a+j] | x[32a+16+j] << 16), fp16/fp32 -> 32 fp32 words (pair j at 2j, 2j+1).
+template <int XT>
+__device__ __forceinline__ void load_x_atom(const void* __restrict__ x, int64_t a, uint32_t* xr) {
+  if constexpr (XT == BF16X_BF16) {
+    const uint16_t* xb = (const uint16_t*)x + 32 * a;
+    const u32x4a v0 = *(const u32x4a*)(xb);
+    const u32x4a v1 = *(const u32x4a*)(xb + 8);
+    const u32x4a v2 = *(const u32x4a*)(xb + 16);
+    const u32x4a v3 = *(const u32x4a*)(xb + 24);
+    const uint32_t lo[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    const uint32_t hi[8] = {v2.x, v2.y, v2.z, v2.w, v3.x, v3.y, v3.z, v3.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xr[2 * i] = perm(hi[i], lo[i], 0x05040100u);
+      xr[2 * i + 1] = perm(hi[i], lo[i], 0x07060302u);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      xr[2 * j] = __float_as_uint(load_x_elem<XT>(x, 32 * a + j));
+      xr[2 * j + 1] = __float_as_uint(load_x_elem<XT>(x, 32 * a + 16 + j));
+    }
+  }
+}
+
+template <int XT>
+__device__ __forceinline__ void dot_atom(const Atom& t, const uint32_t* xr, float& acc0, float& acc1) {
+  uint32_t w[16];
+  decode_pairs(t, w);
+  if constexpr (XT == BF16X_BF16) {
+#pragma unroll
+    for (int j = 0; j < 16; j += 2) {
+      acc0 = dot2_bf16(w[j], xr[j], acc0);
+      acc1 = dot2_bf16(w[j + 1], xr[j + 1], acc1);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      acc0 = fmaf(bf16lo_to_f32(w[j]), __uint_as_float(xr[2 * j]), acc0);
+      acc1 = fmaf(bf16hi_to_f32(w[j]), __uint_as_float(xr[2 * j + 1]), acc1);
+    }
+  }
+}
+
+// (w_exact - w_sat) for a plan entry's exact bits and the element's emax
+__device__ __forceinline__ float entry_delta(uint32_t ent, uint32_t em) {
+  const uint32_t ex = ent & 0xFFFFu;
+  const uint32_t sat = (ex & 0x807Fu) | ((uint32_t)max((int)em - 7, 0) << 7);
+  return bf16lo_to_f32(ex) - bf16lo_to_f32(sat);
+}
+
+// Raw buffer descriptor (gfx9 word 3) over `bytes` bytes at p.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* p, uint64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)n, 0x00020000);
+}
+
+// Atom at byte offsets (vo: this lane's atom within the row, so: the row base;
+// both in atoms) of the four streams, through raw buffer loads.
+__device__ __forceinline__ Atom load_atom_buf(__amdgpu_buffer_rsrc_t rs, __amdgpu_buffer_rsrc_t rm,
+                                              __amdgpu_buffer_rsrc_t rd, __amdgpu_buffer_rsrc_t re,
+                                              uint32_t va, uint32_t sa) {
+  Atom t;
+  const u32x4 m03 = __builtin_amdgcn_raw_buffer_load_b128(rm, (int)(va * 28), (int)(sa * 28), 0);
+  const u32x3 m46 = __builtin_amdgcn_raw_buffer_load_b96(rm, (int)(va * 28 + 16), (int)(sa * 28), 0);
+  const u32x3 d02 = __builtin_amdgcn_raw_buffer_load_b96(rd, (int)(va * 12), (int)(sa * 12), 0);
+  t.s = __builtin_amdgcn_raw_buffer_load_b32(rs, (int)(va * 4), (int)(sa * 4), 0);
+  t.e = __builtin_amdgcn_raw_buffer_load_b16(re, (int)(va * 2), (int)(sa * 2), 0);
+  const uint32_t a0 = m03.x, a1 = m03.y, a2 = m03.z, a3 = m03.w;
+  const uint32_t a4 = m46.x, a5 = m46.y, a6 = m46.z;
+  t.m[0] = a0; t.m[1] = a1; t.m[2] = a2; t.m[3] = a3;
+  t.m[4] = a4; t.m[5] = a5; t.m[6] = a6;
+  const uint32_t b0 = d02.x, b1 = d02.y, b2 = d02.z;
+  t.d[0] = b0; t.d[1] = b1; t.d[2] = b2;
+  return t;
+}
+
+// Sum over the 64 lanes of a wave with DPP: row scans (shr 1, 2, 4, 8) leave
+// each 16-lane row's sum in its lane 15, row_bcast 15/31 fold the rows; the
+// total ends in lane 63.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return v;
+}
+
+// Pipelined decode+GEMV.
+//
+// Work split: a row's P atoms are cut into parts of 64*NS atoms (the last
+// part may be shorter); wave part g of a row owns atoms g*64*NS + 64*s + l
+// for lane l, step s < NS.  G = ceil(P / (64*NS)) waves share a row.
+//
+// LDS holds x once, lane-major: [part][step][chunk][lane] x 16 bytes, so the
+// main loop reads its chunk with one ds_read_b128 at lane*16 + an immediate
+// (conflict free), and the correction overlay finds x[k] by shifts and masks.
+// Plan entries carry a byte of saturated exponent max(emax-7, 0), so the
+// overlay needs no emax gather; row offsets are read with vector loads (a
+// scalar load would share its wait counter with the LDS reads and stall
+// every row on the offsets' latency).  All loads are unconditional (indices
+// clamped): loads under divergent branches make the compiler wait for every
+// outstanding load, which would serialise the prefetch.
+template <int NS, int G, int XT, bool EXACT, bool FULL>
+__global__ __launch_bounds__(256) void gemv_pipe_kernel(
+    const void* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
+    const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
+    const uint32_t* __restrict__ tile_off, const uint32_t* __restrict__ tile_ent,
+    const uint8_t* __restrict__ tile_sat, int64_t out_f, int64_t in_f, int iters, uint16_t* __restrict__ y) {
+  constexpr int RPI = 4 / G;                              // rows per workgroup iteration
+  constexpr int XW = (XT == BF16X_BF16) ? 16 : 32;        // x words per atom
+  constexpr int NC = XW / 4;                              // 16-byte chunks per atom
+  constexpr int NB = NS;                                  // prefetched entry batches per wave
+  constexpr int APW = 64 * NS;                            // atoms per wave part
+  extern __shared__ uint32_t lds[];
+  __shared__ float part[2][4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int rs = wave / G, g = wave - (wave / G) * G;
+  const int64_t P = in_f >> 5;
+
+  // ---- stage x (lane-major pairs)
+  for (int slot = threadIdx.x; slot < G * APW; slot += 256) {
+    const int64_t a = min((int64_t)slot, P - 1);  // slot = part*APW + step*64 + lane = atom index
+    uint32_t xr[XW];
+    load_x_atom<XT>(x, a, xr);
+    u32x4* dst = (u32x4*)lds + (int64_t)((slot >> 6) * NC) * 64 + (slot & 63);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) dst[c * 64] = u32x4{xr[4 * c], xr[4 * c + 1], xr[4 * c + 2], xr[4 * c + 3]};
+  }
+  // x[k] (fp32) from the lane-major layout
+  auto x_at = [&](uint32_t k) -> float {
+    const uint32_t a = k >> 5, j = k & 15, hi = (k >> 4) & 1;
+    const uint32_t chunk_row = (a >> 6) * NC;  // (part*NS + step) * NC
+    if constexpr (XT == BF16X_BF16) {
+      const uint32_t wd = lds[((chunk_row + (j >> 2)) * 64 + (a & 63)) * 4 + (j & 3)];
+      return hi ? bf16hi_to_f32(wd) : bf16lo_to_f32(wd);
+    } else {
+      return __uint_as_float(lds[((chunk_row + (j >> 1)) * 64 + (a & 63)) * 4 + (j & 1) * 2 + hi]);
+    }
+  };
+
+  const __amdgpu_buffer_rsrc_t rs_ = buf_rsrc(sign, (uint64_t)out_f * P * 4);
+  const __amdgpu_buffer_rsrc_t rm_ = buf_rsrc(mant, (uint64_t)out_f * P * 28);
+  const __amdgpu_buffer_rsrc_t rd_ = buf_rsrc(delta, (uint64_t)out_f * P * 12);
+  const __amdgpu_buffer_rsrc_t re_ = buf_rsrc(emax2, (uint64_t)out_f * P * 2);
+  const __amdgpu_buffer_rsrc_t roff = buf_rsrc(tile_off, (uint64_t)(out_f + 1) * 4);
+  uint32_t n_fix = 0;
+  if constexpr (EXACT) n_fix = tile_off[out_f];
+  const __amdgpu_buffer_rsrc_t rent = buf_rsrc(tile_ent, (uint64_t)n_fix * 4);
+  const __amdgpu_buffer_rsrc_t rsat = buf_rsrc(tile_sat, (uint64_t)n_fix);
+
+  // this lane's atoms (fixed for every row), clamped into the row
+  uint32_t va[NS];
+  bool live[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int64_t a = (int64_t)g * APW + 64 * s + lane;
+    live[s] = FULL || a < P;
+    va[s] = (uint32_t)min(a, P - 1);  // idle lanes re-read the row's last atom
+  }
+  const uint32_t ebase = (uint32_t)(g * 64 + lane);  // this lane's entry slot within a row
+
+  auto row_clamp = [&](int64_t rr) { return min(rr, out_f - 1); };
+  auto load_row = [&](int64_t rr, Atom* dst) {
+    const uint32_t sa = (uint32_t)(row_clamp(rr) * P);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) dst[s] = load_atom_buf(rs_, rm_, rd_, re_, va[s], sa);
+  };
+  auto load_off = [&](int64_t rr, uint32_t& b0, uint32_t& b1) {  // vector loads, all lanes alike
+    const int rc = (int)row_clamp(rr);
+    b0 = __builtin_amdgcn_raw_buffer_load_b32(roff, rc * 4, 0, 0);
+    b1 = __builtin_amdgcn_raw_buffer_load_b32(roff, rc * 4 + 4, 0, 0);
+  };
+  auto load_ents = [&](uint32_t b0, uint32_t* ent, uint32_t* sat) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const uint32_t e = b0 + ebase + (uint32_t)(b * 64 * G);  // beyond n_fix reads 0
+      ent[b] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)(e * 4), 0, 0);
+      sat[b] = __builtin_amdgcn_raw_buffer_load_b8(rsat, (int)e, 0, 0);
+    }
+  };
+
+  int64_t r = (int64_t)__builtin_amdgcn_readfirstlane((int)(blockIdx.x * iters * RPI + rs));
+  int64_t rn = r + RPI;
+  uint32_t eb = 0, ee = 0, ebn = 0, een = 0;
+  // two named buffers in ping-pong (a rotation would copy registers whose
+  // loads are still in flight, forcing a wait for them)
+  Atom bufA[NS], bufB[NS];
+  uint32_t entA[NB], entB[NB], satA[NB], satB[NB];
+  if constexpr (EXACT) {
+    eb = tile_off[row_clamp(r)];
+    ee = tile_off[row_clamp(r) + 1];
+    load_ents(eb, entA, satA);
+    load_off(rn, ebn, een);
+  }
+  load_row(r, bufA);
+  __syncthreads();
+
+  const u32x4* xl = (const u32x4*)lds + (int64_t)(g * NS) * NC * 64 + lane;
+  auto body = [&](auto prefetch, int it, Atom* cur, uint32_t* ent, uint32_t* sat, Atom* nxt, uint32_t* entn,
+                  uint32_t* satn) {
+    constexpr bool PF = decltype(prefetch)::value;
+    // prefetch: offsets two rows ahead, then the next row's entries and atoms
+    const int64_t rnn = rn + RPI;
+    uint32_t ebnn = 0, eenn = 0;
+    if constexpr (PF) {
+      if constexpr (EXACT) {
+        load_off(rnn, ebnn, eenn);
+        load_ents(ebn, entn, satn);
+      }
+      load_row(rn, nxt);
+    }
+    // decode + dot of this row
+    float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      uint32_t xr[XW];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        const u32x4 v = xl[(s * NC + c) * 64];
+        xr[4 * c] = v.x; xr[4 * c + 1] = v.y; xr[4 * c + 2] = v.z; xr[4 * c + 3] = v.w;
+      }
+      if constexpr (FULL) {
+        dot_atom<XT>(cur[s], xr, acc0, acc1);
+      } else {
+        float t0 = 0.f, t1 = 0.f;
+        dot_atom<XT>(cur[s], xr, t0, t1);
+        acc0 += live[s] ? t0 : 0.f;
+        acc1 += live[s] ? t1 : 0.f;
+      }
+    }
+    // correction overlay: (w_exact - w_sat) * x[k]
+    if constexpr (EXACT) {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const uint32_t e = eb + ebase + (uint32_t)(b * 64 * G);
+        const uint32_t k = min(ent[b] >> 16, (uint32_t)in_f - 1);
+        const uint32_t sbits = (ent[b] & 0x807Fu) | (sat[b] << 7);
+        const float c = (bf16lo_to_f32(ent[b]) - bf16lo_to_f32(sbits)) * x_at(k);
+        acc0 += (e < ee) ? c : 0.f;
+      }
+      // rows with more entries than the prefetched batches (rare)
+      for (uint32_t e = eb + ebase + (uint32_t)(NB * 64 * G); e < ee; e += 64 * G) {
+        const uint32_t en = tile_ent[e];
+        const uint32_t k = min(en >> 16, (uint32_t)in_f - 1);
+        const uint32_t sbits = (en & 0x807Fu) | ((uint32_t)tile_sat[e] << 7);
+        acc0 = fmaf(bf16lo_to_f32(en) - bf16lo_to_f32(sbits), x_at(k), acc0);
+      }
+    }
+    // reduce and store
+    const float tot = wave_sum_dpp(acc0 + acc1);
+    if constexpr (G == 1) {
+      if (lane == 63 && r < out_f) y[r] = (uint16_t)f32_to_bf16_rne(tot);
+    } else {
+      if (lane == 63) part[it & 1][wave] = tot;
+      __syncthreads();
+      if (g == 0 && lane == 0 && r < out_f) {
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < G; ++i) sum += part[it & 1][rs * G + i];
+        y[r] = (uint16_t)f32_to_bf16_rne(sum);
+      }
+    }
+    eb = ebn; ee = een; ebn = ebnn; een = eenn;
+    r = rn; rn = rnn;
+  };
+  int it = 0;
+  for (; it + 2 < iters; it += 2) {
+    body(std::true_type{}, it, bufA, entA, satA, bufB, entB, satB);
+    body(std::true_type{}, it + 1, bufB, entB, satB, bufA, entA, satA);
+  }
+  if (iters - it == 2) {
+    body(std::true_type{}, it, bufA, entA, satA, bufB, entB, satB);
+    body(std::false_type{}, it + 1, bufB, entB, satB, bufA, entA, satA);
+  } else {
+    body(std::false_type{}, it, bufA, entA, satA, bufB, entB, satB);
+  }
+}
+
+// Any in_f % 32 == 0 (e.g. beyond the pipelined kernel's 16384 columns):
+// one wave per row, x values read from global memory per atom.
+template <int XT>
+__global__ __launch_bounds__(256) void gemv_generic_kernel(
+    const void* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
+    const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
+    const uint32_t* __restrict__ tile_off, const uint32_t* __restrict__ tile_ent, int64_t out_f,
+    int64_t in_f, int tpr, uint16_t* __restrict__ y) {
+  constexpr int XW = (XT == BF16X_BF16) ? 16 : 32;
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= out_f) return;
+  const int64_t P = in_f >> 5;
+  const uint8_t* emax = (const uint8_t*)emax2;
+  float acc0 = 0.f, acc1 = 0.f;
+  for (int64_t a = lane; a < P; a += 64) {
+    uint32_t xr[XW];
+    load_x_atom<XT>(x, a, xr);
+    dot_atom<XT>(load_atom(sign, mant, delta, emax2, r * P + a), xr, acc0, acc1);
+  }
+  if (tile_off != nullptr) {
+    for (int seg = 0; seg < tpr; ++seg) {
+      const int64_t t = r * tpr + seg;
+      for (int64_t e = (int64_t)tile_off[t] + lane; e < (int64_t)tile_off[t + 1]; e += 64) {
+        const uint32_t en = tile_ent[e];
+        const int64_t k = (int64_t)seg * kPlanTileCols + (en >> 16);
+        if (k < in_f) acc0 = fmaf(entry_delta(en, emax[(r * in_f + k) >> 4]), load_x_elem<XT>(x, k), acc0);
+      }
+    }
+  }
+  const float tot = wave_sum(acc0 + acc1);
+  if (lane == 0) y[r] = (uint16_t)f32_to_bf16_rne(tot);
+}
+
+}  // namespace bf16x
+
+using namespace bf16x;
+
+namespace {
+
+// Launch-shape overrides for tuning sweeps (BF16X_GEMV_ITERS, BF16X_GEMV_G);
+// read once per process, 0 = use the built-in heuristic.
+int env_int(const char* name) {
+  const char* s = getenv(name);
+  return s ? atoi(s) : 0;
+}
+int gemv_iters_override() {
+  static int v = env_int("BF16X_GEMV_ITERS");
+  return v;
+}
+int gemv_g_override() {
+  static int v = env_int("BF16X_GEMV_G");
+  return v;
+}
+
+template <int XT>
+int launch_gemv(const void* x, const uint32_t* sign, const uint32_t* mant, const uint32_t* delta,
+                const uint16_t* emax2, const uint32_t* to, const uint32_t* te, const uint8_t* ts, int64_t out_f,
+                int64_t in_f, uint16_t* y, hipStream_t st) {
+  const int64_t P = in_f >> 5;
+  const int tpr = tiles_per_row(in_f);
+  // parts of 64*NS atoms per wave; G = ceil(P / (64*NS)) waves per row.
+  // NS = 2 unless rows are few (then 1, for more waves in flight).
+  int NS = (P > 64) ? 2 : 1;
+  int G = (int)((P + 64 * NS - 1) / (64 * NS));
+  if (NS == 2 && out_f * G < 4096 && (P + 63) / 64 <= 4) { NS = 1; G = (int)((P + 63) / 64); }
+  if (G == 3) G = 4;  // the fourth part of each row is empty
+  const int g_req = gemv_g_override();
+  if (g_req == 1 || g_req == 2 || g_req == 4) {
+    const int ns_req = (P + 64 * g_req - 1) / (64 * g_req);
+    if (ns_req >= 1 && ns_req <= 2) { NS = ns_req; G = g_req; }
+  }
+  const int xw = (XT == BF16X_BF16) ? 16 : 32;
+  const size_t lds = (size_t)G * NS * 64 * (xw / 4) * 16;
+  if (G <= 4 && tpr == 1 && (out_f + 1) * P * 28 < (int64_t)0xFFFFFFFF && lds + 64 <= 65536) {
+    const bool full = (XT == BF16X_BF16) && P == (int64_t)G * 64 * NS;
+    const int rpi = 4 / G;
+    const int64_t groups = (out_f + rpi - 1) / rpi;
+    int iters = gemv_iters_override();
+    if (iters <= 0) iters = groups >= 2048 ? 2 : 1;
+    const int64_t grid = (groups + iters - 1) / iters;
+    if (grid > INT32_MAX) return BF16X_ESHAPE;
+#define BF16X_PIPE1(NS_, G_, EX_, FULL_)                                                                \
+  hipLaunchKernelGGL((gemv_pipe_kernel<NS_, G_, XT, EX_, FULL_>), dim3((unsigned)grid), dim3(256), lds, st, x, \
+                     sign, mant, delta, emax2, to, te, ts, out_f, in_f, iters, y)
+#define BF16X_PIPE(NS_, G_)                                                                            \
+  do {                                                                                               \
+    if (to != nullptr) {                                                                             \
+      if (full) BF16X_PIPE1(NS_, G_, true, (XT == BF16X_BF16)); else BF16X_PIPE1(NS_, G_, true, false); \
+    } else {                                                                                         \
+      if (full) BF16X_PIPE1(NS_, G_, false, (XT == BF16X_BF16)); else BF16X_PIPE1(NS_, G_, false, false); \
+    }                                                                                                \
+  } while (0)
+    if (NS == 1) {
+      if (G == 1) BF16X_PIPE(1, 1); else if (G == 2) BF16X_PIPE(1, 2); else BF16X_PIPE(1, 4);
+    } else {
+      if (G == 1) BF16X_PIPE(2, 1); else if (G == 2) BF16X_PIPE(2, 2); else BF16X_PIPE(2, 4);
+    }
+#undef BF16X_PIPE
+#undef BF16X_PIPE1
+  } else {
+    const int64_t grid = (out_f + 3) / 4;
+    if (grid > INT32_MAX) return BF16X_ESHAPE;
+    hipLaunchKernelGGL((gemv_generic_kernel<XT>), dim3((unsigned)grid), dim3(256), 0, st, x, sign, mant, delta,
+                       emax2, to, te, out_f, in_f, tpr, y);
+  }
+  return launch_status();
+}
+
+}  // namespace
+
+extern "C" int bf16x_gemv(const void* x, int32_t x_dtype, const int32_t* sign, int64_t n_sign,
+                          const int32_t* mant, int64_t n_mant, const int32_t* delta, int64_t n_delta,
+                          const uint8_t* emax, int64_t n_emax, const uint32_t* tile_off,
+                          const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f, int64_t in_f,
+                          int32_t sub, int32_t mode, uint16_t* y, bf16x_stream_t stream) {
+  if (!x || !sign || !mant || !delta || !emax || !y) return BF16X_EARG;
+  if (mode != BF16X_EXACT && mode != BF16X_SATURATED) return BF16X_EARG;
+  if (mode == BF16X_EXACT && (!tile_off || !tile_ent || !tile_sat)) return BF16X_EARG;
+  if (x_dtype != BF16X_BF16 && x_dtype != BF16X_F16 && x_dtype != BF16X_F32) return BF16X_EDTYPE;
+  int rc = check_dict(out_f, in_f, sub, n_sign, n_mant, n_delta, n_emax);
+  if (rc) return rc;
+  if ((in_f & 31) != 0) return BF16X_ESHAPE;
+  if (!aligned4(sign) || !aligned4(mant) || !aligned4(delta) || !aligned2(emax) || !aligned4(x)) return BF16X_EARG;
+  const uint32_t* to = (mode == BF16X_EXACT) ? tile_off : nullptr;
+  const uint32_t* te = (mode == BF16X_EXACT) ? tile_ent : nullptr;
+  const uint8_t* ts = (mode == BF16X_EXACT) ? tile_sat : nullptr;
+  hipStream_t st = (hipStream_t)stream;
+  const uint32_t* s = (const uint32_t*)sign;
+  const uint32_t* m = (const uint32_t*)mant;
+  const uint32_t* d = (const uint32_t*)delta;
+  const uint16_t* e = (const uint16_t*)emax;
+  switch (x_dtype) {
+    case BF16X_BF16: return launch_gemv<BF16X_BF16>(x, s, m, d, e, to, te, ts, out_f, in_f, y, st);
+    case BF16X_F16: return launch_gemv<BF16X_F16>(x, s, m, d, e, to, te, ts, out_f, in_f, y, st);
+    default: return launch_gemv<BF16X_F32>(x, s, m, d, e, to, te, ts, out_f, in_f, y, st);
+  }
+}

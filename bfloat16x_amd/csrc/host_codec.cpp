@@ -158,7 +158,8 @@ extern "C" int bf16x_plan_host(const int32_t* ovf_idx, const uint8_t* ovf_val, i
                                const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
                                const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
                                int64_t out_f, int64_t in_f, int32_t check,
-                               uint32_t* tile_off, uint32_t* tile_ent, int64_t ent_cap, int64_t* n_fix) {
+                               uint32_t* tile_off, uint32_t* tile_ent, uint8_t* tile_sat, int64_t ent_cap,
+                               int64_t* n_fix) {
   if (!sign || !mant || !emax || !tile_off || !n_fix) return BF16X_EARG;
   if (n_ovf < 0 || (n_ovf > 0 && (!ovf_idx || !ovf_val))) return BF16X_EARG;
   if (check && !delta) return BF16X_EARG;
@@ -203,7 +204,7 @@ extern "C" int bf16x_plan_host(const int32_t* ovf_idx, const uint8_t* ovf_val, i
   if (kept > (int64_t)UINT32_MAX) return BF16X_ESHAPE;
   for (int64_t t = 0; t < n_tiles; ++t) tile_off[t + 1] += tile_off[t];
   if (kept > ent_cap) return BF16X_ECAPACITY;
-  if (kept > 0 && !tile_ent) return BF16X_EARG;
+  if (kept > 0 && (!tile_ent || !tile_sat)) return BF16X_EARG;
   // pass 2: entries in table order (ascending position = tile order, then column)
   int64_t o = 0;
   for (int64_t j = 0; j < n_ovf; ++j) {
@@ -213,7 +214,9 @@ extern "C" int bf16x_plan_host(const int32_t* ovf_idx, const uint8_t* ovf_val, i
     const int64_t col = (p % in_f) % kTileCols;
     const uint32_t s = get_bits(sign, n_sign, p, 1);
     const uint32_t m = get_bits(mant, n_mant, p * 7, 7);
-    const uint32_t e = (uint32_t)((int)emax[p / 16] - v) & 0xFFu;  // opqk_linear.py:375
+    const int em = emax[p / 16];
+    const uint32_t e = (uint32_t)(em - v) & 0xFFu;  // opqk_linear.py:375
+    tile_sat[o] = (uint8_t)std::max(em - 7, 0);
     tile_ent[o++] = ((uint32_t)col << 16) | (s << 15) | (e << 7) | m;
   }
   return BF16X_OK;

@@ -19,4 +19,21 @@ inline int launch_status() {
   return e == hipSuccess ? BF16X_OK : (int)e;
 }
 
+constexpr int64_t kPlanTileCols = 65536;
+
+// Shape / stream-length validation shared by every packed-dict entry point.
+inline int check_dict(int64_t out_f, int64_t in_f, int32_t sub, int64_t n_sign, int64_t n_mant, int64_t n_delta,
+                      int64_t n_emax) {
+  if (out_f <= 0 || in_f <= 0) return BF16X_ESHAPE;
+  if (sub != 16) return BF16X_ESUB;
+  const int64_t N = out_f * in_f;
+  if (N > ((int64_t)1 << 36)) return BF16X_ESHAPE;
+  if (n_sign < bf16x_stream_words(N, 1) || n_mant < bf16x_stream_words(N, 7) ||
+      n_delta < bf16x_stream_words(N, 3) || n_emax < (N + 15) / 16)
+    return BF16X_ESTREAM_LEN;
+  return BF16X_OK;
+}
+
+inline int tiles_per_row(int64_t in_f) { return (int)((in_f + kPlanTileCols - 1) / kPlanTileCols); }
+
 }  // namespace

@@ -130,7 +130,8 @@ def bf16x_gemv(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None =
     st = _lib.lib().bf16x_gemv(xx.data_ptr(), _X_DTYPES[xx.dtype], s.data_ptr(), s.numel(), m.data_ptr(),
                                m.numel(), d.data_ptr(), d.numel(), e.data_ptr(), e.numel(),
                                _lib.ptr(plan.tile_off) if plan else None, _lib.ptr(plan.tile_ent) if plan else None,
-                               out_f, in_f, int(sub), mode, y.data_ptr(), _lib.stream_of(s.device))
+                               _lib.ptr(plan.tile_sat) if plan else None, out_f, in_f, int(sub), mode, y.data_ptr(),
+                               _lib.stream_of(s.device))
     _lib.check(st, "bf16x_gemv")
     return y
 

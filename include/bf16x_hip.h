@@ -21,9 +21,11 @@
  *    streams padded with extra words (the reference's _pad1) are accepted.
  *  - Overflow plan: the sparse table entries whose true delta exceeds 7,
  *    grouped per tile (tile = one row, or one 65536-column segment of a row
- *    when in_f > 65536):
+ *    when in_f > 65536), for emax runs of 16 elements:
  *      tile_off uint32 [n_tiles + 1]  CSR offsets into tile_ent
  *      tile_ent uint32 [n_fix]        (column within tile << 16) | exact bf16 bits
+ *      tile_sat uint8  [n_fix]        saturated exponent max(emax - 7, 0) of the
+ *                                     entry's element (used by the GEMV overlay)
  *    Built by bf16x_plan_host() or bf16x_plan_from_csr().
  *  - All device work is enqueued on `stream` (a hipStream_t; NULL = the
  *    default stream) and is asynchronous.
@@ -98,19 +100,20 @@ int bf16x_plan_host(const int32_t* ovf_idx, const uint8_t* ovf_val, int64_t n_ov
                     const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
                     const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
                     int64_t out_f, int64_t in_f, int32_t check,
-                    uint32_t* tile_off, uint32_t* tile_ent, int64_t ent_cap, int64_t* n_fix);
+                    uint32_t* tile_off, uint32_t* tile_ent, uint8_t* tile_sat, int64_t ent_cap,
+                    int64_t* n_fix);
 
 /* ------------------------------------------------------------------------
  * Device plan from the reference's per-row CSR (olk col int32, old true
  * delta int32, oloff int32 [out_f + 1]) -- the arguments of
  * bf16x_fused_gemv (bf16x_fused.py:114) built at bf16x_fused.py:165-179.
- * Writes tile_ent (dev, oloff[out_f] entries); tile_off is oloff itself
- * (requires in_f <= 65536).  All pointers dev.
+ * Writes tile_ent and tile_sat (dev, n_entries = oloff[out_f] each); tile_off
+ * is oloff itself (requires in_f <= 65536).  All pointers dev.
  * ------------------------------------------------------------------------ */
 int bf16x_plan_from_csr(const int32_t* olk, const int32_t* old, const int32_t* oloff,
                         const int32_t* sign, const int32_t* mant, const uint8_t* emax,
                         int64_t out_f, int64_t in_f, int64_t n_entries,
-                        uint32_t* tile_ent, bf16x_stream_t stream);
+                        uint32_t* tile_ent, uint8_t* tile_sat, bf16x_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * One-pass decode.  Replaces bf16x_decode_triton (bf16x_triton_test.py:80-108)
@@ -129,13 +132,14 @@ int bf16x_decode(const int32_t* sign, int64_t n_sign, const int32_t* mant, int64
  * Fused decode + GEMV, batch 1.  Replaces bf16x_fused_gemv
  * (bf16x_fused.py:114-127) / _bf16x_gemv_fused_kernel (:32-111):
  * y[n] = sum_k W[n,k] * x[k], fp32 accumulation, y stored as bf16.
- * x: dev [in_f] of x_dtype.  mode EXACT applies the plan, SATURATED not.
- * Requires in_f % 32 == 0.  All pointers dev.
+ * x: dev [in_f] of x_dtype.  mode EXACT applies the plan (tile_off,
+ * tile_ent, tile_sat), SATURATED ignores it.  Requires in_f % 32 == 0.
+ * All pointers dev.
  * ------------------------------------------------------------------------ */
 int bf16x_gemv(const void* x, int32_t x_dtype,
                const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
                const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
-               const uint32_t* tile_off, const uint32_t* tile_ent,
+               const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat,
                int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
                uint16_t* y, bf16x_stream_t stream);
 

@@ -150,13 +150,13 @@ def test_gpu_entry_points_validate_before_launch():
     assert lib.bf16x_decode(fake, ws, fake, wm, fake, wd, fake, ne, None, None, 64, 64, 16, 1, None,
                             None) == _lib.EARG
     # GEMV: bad dtype, in_f % 32
-    assert lib.bf16x_gemv(fake, 7, fake, ws, fake, wm, fake, wd, fake, ne, None, None, 64, 64, 16, 1, fake,
+    assert lib.bf16x_gemv(fake, 7, fake, ws, fake, wm, fake, wd, fake, ne, None, None, None, 64, 64, 16, 1, fake,
                           None) == _lib.EDTYPE
     n2 = 64 * 48
     assert lib.bf16x_gemv(fake, 0, fake, dc.stream_words(n2, 1), fake, dc.stream_words(n2, 7), fake,
-                          dc.stream_words(n2, 3), fake, n2 // 16, None, None, 64, 48, 16, 1, fake,
+                          dc.stream_words(n2, 3), fake, n2 // 16, None, None, None, 64, 48, 16, 1, fake,
                           None) == _lib.ESHAPE
-    assert lib.bf16x_gemv(fake, 0, fake, ws, fake, wm, fake, wd, fake, ne, None, None, 0, 64, 16, 1, fake,
+    assert lib.bf16x_gemv(fake, 0, fake, ws, fake, wm, fake, wd, fake, ne, None, None, None, 0, 64, 16, 1, fake,
                           None) == _lib.ESHAPE
 
 
