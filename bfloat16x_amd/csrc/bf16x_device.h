@@ -41,7 +41,8 @@ struct Atom {
   uint32_t s;       // sign word
   uint32_t m[7];    // mantissa words
   uint32_t d[3];    // 3-bit code words
-  uint32_t e;       // emax byte of half 0 | emax byte of half 1 << 8
+  uint16_t e;       // emax byte of half 0 | emax byte of half 1 << 8 (kept 16-bit:
+                    // a widened copy would be made where the load lands)
 };
 
 __device__ __forceinline__ uint32_t alignbit(uint32_t hi, uint32_t lo, uint32_t sh) {
@@ -106,7 +107,8 @@ __device__ __forceinline__ void decode_pairs(const Atom& t, uint32_t out[16]) {
   pd[1] = alignbit(t.d[2], t.d[0], 16);
   pd[2] = lo_hi(t.d[1], t.d[2]);
   // emax of each half at bits 7..14 of its 16-bit lane
-  const uint32_t E = ((t.e & 0xFFu) << 7) | ((t.e & 0xFF00u) << 15);
+  const uint32_t e16 = t.e;
+  const uint32_t E = ((e16 & 0xFFu) << 7) | ((e16 & 0xFF00u) << 15);
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     // mantissa field at lane bit 7j

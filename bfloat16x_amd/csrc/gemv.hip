@@ -157,15 +157,6 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
   const int rs = wave / G, g = wave - (wave / G) * G;
   const int64_t P = in_f >> 5;
 
-  // ---- stage x (lane-major pairs)
-  for (int slot = threadIdx.x; slot < G * APW; slot += 256) {
-    const int64_t a = min((int64_t)slot, P - 1);  // slot = part*APW + step*64 + lane = atom index
-    uint32_t xr[XW];
-    load_x_atom<XT>(x, a, xr);
-    u32x4* dst = (u32x4*)lds + (int64_t)((slot >> 6) * NC) * 64 + (slot & 63);
-#pragma unroll
-    for (int c = 0; c < NC; ++c) dst[c * 64] = u32x4{xr[4 * c], xr[4 * c + 1], xr[4 * c + 2], xr[4 * c + 3]};
-  }
   // x[k] (fp32) from the lane-major layout
   auto x_at = [&](uint32_t k) -> float {
     const uint32_t a = k >> 5, j = k & 15, hi = (k >> 4) & 1;
@@ -183,10 +174,10 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
   const __amdgpu_buffer_rsrc_t rd_ = buf_rsrc(delta, (uint64_t)out_f * P * 12);
   const __amdgpu_buffer_rsrc_t re_ = buf_rsrc(emax2, (uint64_t)out_f * P * 2);
   const __amdgpu_buffer_rsrc_t roff = buf_rsrc(tile_off, (uint64_t)(out_f + 1) * 4);
-  uint32_t n_fix = 0;
-  if constexpr (EXACT) n_fix = tile_off[out_f];
-  const __amdgpu_buffer_rsrc_t rent = buf_rsrc(tile_ent, (uint64_t)n_fix * 4);
-  const __amdgpu_buffer_rsrc_t rsat = buf_rsrc(tile_sat, (uint64_t)n_fix);
+  // entry reads are clamped into [.., row end - 1] (see load_ents), so these
+  // descriptors need no length: the plan holds at least one entry word
+  const __amdgpu_buffer_rsrc_t rent = buf_rsrc(tile_ent, 0xFFFFFFFFull);
+  const __amdgpu_buffer_rsrc_t rsat = buf_rsrc(tile_sat, 0xFFFFFFFFull);
 
   // this lane's atoms (fixed for every row), clamped into the row
   uint32_t va[NS];
@@ -210,34 +201,64 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
     b0 = __builtin_amdgcn_raw_buffer_load_b32(roff, rc * 4, 0, 0);
     b1 = __builtin_amdgcn_raw_buffer_load_b32(roff, rc * 4 + 4, 0, 0);
   };
-  auto load_ents = [&](uint32_t b0, uint32_t* ent, uint32_t* sat) {
+  auto load_ents = [&](uint32_t b0, uint32_t b1, uint32_t* ent, uint8_t* sat) {
+    const uint32_t last = b1 > 0 ? b1 - 1 : 0;  // slots past the row end re-read a valid entry
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const uint32_t e = b0 + ebase + (uint32_t)(b * 64 * G);  // beyond n_fix reads 0
+      const uint32_t e = min(b0 + ebase + (uint32_t)(b * 64 * G), last);
       ent[b] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)(e * 4), 0, 0);
       sat[b] = __builtin_amdgcn_raw_buffer_load_b8(rsat, (int)e, 0, 0);
     }
   };
 
-  int64_t r = (int64_t)__builtin_amdgcn_readfirstlane((int)(blockIdx.x * iters * RPI + rs));
+  // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs
+  // (block b runs on XCD b % 8); give each XCD a contiguous range of rows so
+  // the small per-row plan chunks of neighbouring rows share its L2.
+  const int nb = (int)gridDim.x;
+  const int b = (int)blockIdx.x;
+  const int per = nb / 8, extra = nb - per * 8;  // XCD x gets per (+1 if x < extra) blocks
+  const int xcd = b & 7, slot_in_xcd = b >> 3;
+  const int lb = (nb >= 8) ? (xcd * per + min(xcd, extra) + slot_in_xcd) : b;
+  int64_t r = (int64_t)__builtin_amdgcn_readfirstlane((int)((int64_t)lb * iters * RPI + rs));
   int64_t rn = r + RPI;
   uint32_t eb = 0, ee = 0, ebn = 0, een = 0;
   // two named buffers in ping-pong (a rotation would copy registers whose
   // loads are still in flight, forcing a wait for them)
   Atom bufA[NS], bufB[NS];
-  uint32_t entA[NB], entB[NB], satA[NB], satB[NB];
+  uint32_t entA[NB], entB[NB];
+  uint8_t satA[NB], satB[NB];  // kept 8-bit (see Atom::e)
+  // prologue, in the order the first row needs its data (vector loads
+  // complete in issue order, so a wait for a load also waits for every load
+  // issued before it): row offsets, this thread's x values, the row's atoms,
+  // then the entries (which need the offsets)
   if constexpr (EXACT) {
-    eb = tile_off[row_clamp(r)];
-    ee = tile_off[row_clamp(r) + 1];
-    load_ents(eb, entA, satA);
+    load_off(r, eb, ee);
     load_off(rn, ebn, een);
   }
+  constexpr int XSLOTS = (G * APW + 255) / 256;  // x atoms staged per thread (<= 2)
+  uint32_t xs_reg[XSLOTS][XW];
+#pragma unroll
+  for (int i = 0; i < XSLOTS; ++i) {
+    const int slot = threadIdx.x + 256 * i;
+    load_x_atom<XT>(x, min((int64_t)slot, P - 1), xs_reg[i]);  // slot index = atom index
+  }
   load_row(r, bufA);
+#pragma unroll
+  for (int i = 0; i < XSLOTS; ++i) {
+    const int slot = threadIdx.x + 256 * i;
+    if (slot < G * APW) {
+      u32x4* dst = (u32x4*)lds + (int64_t)((slot >> 6) * NC) * 64 + (slot & 63);
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        dst[c * 64] = u32x4{xs_reg[i][4 * c], xs_reg[i][4 * c + 1], xs_reg[i][4 * c + 2], xs_reg[i][4 * c + 3]};
+    }
+  }
+  if constexpr (EXACT) load_ents(eb, ee, entA, satA);
   __syncthreads();
 
   const u32x4* xl = (const u32x4*)lds + (int64_t)(g * NS) * NC * 64 + lane;
-  auto body = [&](auto prefetch, int it, Atom* cur, uint32_t* ent, uint32_t* sat, Atom* nxt, uint32_t* entn,
-                  uint32_t* satn) {
+  auto body = [&](auto prefetch, int it, Atom* cur, uint32_t* ent, uint8_t* sat, Atom* nxt, uint32_t* entn,
+                  uint8_t* satn) {
     constexpr bool PF = decltype(prefetch)::value;
     // prefetch: offsets two rows ahead, then the next row's entries and atoms
     const int64_t rnn = rn + RPI;
@@ -245,10 +266,13 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
     if constexpr (PF) {
       if constexpr (EXACT) {
         load_off(rnn, ebnn, eenn);
-        load_ents(ebn, entn, satn);
+        load_ents(ebn, een, entn, satn);
       }
       load_row(rn, nxt);
     }
+    // keep the prefetch ahead of the decode: without this the scheduler sinks
+    // the loads below the waits for this row's data and the pipeline drains
+    __builtin_amdgcn_sched_barrier(0);
     // decode + dot of this row
     float acc0 = 0.f, acc1 = 0.f;
 #pragma unroll
@@ -274,7 +298,7 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
       for (int b = 0; b < NB; ++b) {
         const uint32_t e = eb + ebase + (uint32_t)(b * 64 * G);
         const uint32_t k = min(ent[b] >> 16, (uint32_t)in_f - 1);
-        const uint32_t sbits = (ent[b] & 0x807Fu) | (sat[b] << 7);
+        const uint32_t sbits = (ent[b] & 0x807Fu) | ((uint32_t)sat[b] << 7);
         const float c = (bf16lo_to_f32(ent[b]) - bf16lo_to_f32(sbits)) * x_at(k);
         acc0 += (e < ee) ? c : 0.f;
       }
