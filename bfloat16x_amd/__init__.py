@@ -4,14 +4,17 @@ Call surface (mirrors the reference dfytensor/bfloat16x):
   bf16x_quantize                       opqk_linear.py:291
   bf16x_decode / bf16x_decode_triton   bf16x_triton_test.py:80
   bf16x_fused_gemv                     bf16x_fused.py:114
+  bf16x_fused_gemm                     bf16x_gemm_fused.py:97
 All GPU work runs in the HIP library libbf16x_hip.so through its C ABI
 (include/bf16x_hip.h).
 """
 from ._lib import Bf16xError, version
 from .codec import Bf16xPlan, bf16x_quantize, build_plan_host, stream_words
-from .ops import bf16x_decode, bf16x_decode_triton, bf16x_fused_gemv, bf16x_gemv
+from .ops import (bf16x_decode, bf16x_decode_triton, bf16x_fused_gemm, bf16x_fused_gemv, bf16x_gemm,
+                  bf16x_gemv)
 
 __all__ = [
-    "Bf16xError", "Bf16xPlan", "bf16x_decode", "bf16x_decode_triton", "bf16x_fused_gemv", "bf16x_gemv",
+    "Bf16xError", "Bf16xPlan", "bf16x_decode", "bf16x_decode_triton", "bf16x_fused_gemm", "bf16x_fused_gemv",
+    "bf16x_gemm", "bf16x_gemv",
     "bf16x_quantize", "build_plan_host", "stream_words", "version",
 ]

@@ -38,6 +38,11 @@ PROTOTYPES = {
                                     _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
     "bf16x_gemv": (ctypes.c_int, [_P, _c_i32, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P, _P,
                                   _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
+    "bf16x_kplan_size": (_c_i64, [_c_i64, _c_i64]),
+    "bf16x_kplan_build": (ctypes.c_int, [_P, _P, _c_i64, _c_i64, _P, _P, _P]),
+    "bf16x_gemm_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "bf16x_gemm": (ctypes.c_int, [_P, _c_i32, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P,
+                                  _c_i64, _c_i64, _c_i32, _c_i32, _P, _c_i32, _P, _c_i64, _P]),
 }
 
 _LIB = None

@@ -72,17 +72,39 @@ def bf16x_quantize(w: torch.Tensor, sub: int = SUB, n_threads: int = 0) -> dict:
 @dataclass
 class Bf16xPlan:
     """Device overflow plan: tile_off uint32 [n_tiles+1], tile_ent uint32 [n_fix]
-    ((column << 16) | exact bits), tile_sat uint8 [n_fix] (max(emax - 7, 0))."""
+    ((column << 16) | exact bits), tile_sat uint8 [n_fix] (max(emax - 7, 0)).
+    kp_off / kp_ent: the step-major regrouping used by the GEMM, built on the
+    device on first use (see kplan())."""
     tile_off: torch.Tensor
     tile_ent: torch.Tensor
     tile_sat: torch.Tensor
     n_fix: int
     out_f: int
     in_f: int
+    kp_off: torch.Tensor | None = None
+    kp_ent: torch.Tensor | None = None
 
     @property
     def nbytes(self) -> int:
-        return self.tile_off.numel() * 4 + self.tile_ent.numel() * 4 + self.tile_sat.numel()
+        n = self.tile_off.numel() * 4 + self.tile_ent.numel() * 4 + self.tile_sat.numel()
+        if self.kp_off is not None:
+            n += self.kp_off.numel() * 4 + self.kp_ent.numel() * 4
+        return n
+
+    def kplan(self):
+        """(kp_off, kp_ent) on the plan's device, built once by bf16x_kplan_build."""
+        if self.kp_off is None:
+            dev = self.tile_off.device
+            if not self.tile_off.is_cuda:
+                raise ValueError("kplan(): the plan must live on the GPU")
+            size = int(_lib.lib().bf16x_kplan_size(self.out_f, self.in_f))
+            kp_off = torch.empty(max(size, 1), dtype=torch.int32, device=dev)
+            kp_ent = torch.zeros(max(self.n_fix, 1), dtype=torch.int32, device=dev)
+            st = _lib.lib().bf16x_kplan_build(self.tile_off.data_ptr(), self.tile_ent.data_ptr(), self.out_f,
+                                              self.in_f, kp_off.data_ptr(), kp_ent.data_ptr(), _lib.stream_of(dev))
+            _lib.check(st, "bf16x_kplan_build")
+            self.kp_off, self.kp_ent = kp_off, kp_ent
+        return self.kp_off, self.kp_ent
 
     def to(self, device) -> "Bf16xPlan":
         return Bf16xPlan(self.tile_off.to(device), self.tile_ent.to(device), self.tile_sat.to(device),

@@ -2,6 +2,7 @@
 
 bf16x_decode / bf16x_decode_triton  <- bf16x_triton_test.py:80-108
 bf16x_fused_gemv                    <- bf16x_fused.py:114-127
+bf16x_fused_gemm                    <- bf16x_gemm_fused.py:97-114
 
 Every wrapper validates its tensors on the host, then calls one C-ABI entry
 point of libbf16x_hip.so on torch's current stream.  There is no fallback:
@@ -150,3 +151,68 @@ def bf16x_fused_gemv(x, sign, mant, delta, emax, olk, old, oloff, out_f, in_f, g
         s, m, _, e = _streams(sign, mant, delta, emax)
         plan = plan_for_csr(olk, old, _dev_tensor(oloff, "oloff", (torch.int32,)), s, m, e, out_f, in_f)
     return bf16x_gemv(x, sign, mant, delta, emax, out_f, in_f, plan=plan)
+
+
+def _gemm_launch(x2, s, m, d, e, out_f, in_f, plan, y, y_dtype, sub=16):
+    mode = _lib.SATURATED if plan is None else _lib.EXACT
+    kp_off, kp_ent = plan.kplan() if plan is not None else (None, None)
+    L = _lib.lib()
+    ws_bytes = int(L.bf16x_gemm_workspace(x2.shape[0], out_f, in_f))
+    ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=x2.device) if ws_bytes else None
+    st = L.bf16x_gemm(x2.data_ptr(), _lib.BF16, x2.shape[0], s.data_ptr(), s.numel(), m.data_ptr(),
+                      m.numel(), d.data_ptr(), d.numel(), e.data_ptr(), e.numel(), _lib.ptr(kp_off),
+                      _lib.ptr(kp_ent), out_f, in_f, int(sub), mode, y.data_ptr(), y_dtype,
+                      _lib.ptr(ws), ws_bytes, _lib.stream_of(s.device))
+    _lib.check(st, "bf16x_gemm")
+
+
+def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None = None, sub=16) -> torch.Tensor:
+    """y[..., out_f] = x[..., in_f] . W^T with W decoded on the fly, in x's dtype.
+
+    Exact with a plan, saturated without one.  bf16 activations run one bf16
+    MFMA pass; fp16/fp32 activations are split as x = hi + lo (two bf16
+    tensors, exact for fp16, 16 mantissa bits for fp32) and accumulated over
+    two passes in fp32.  Shapes outside the fused kernel (in_f not a multiple
+    of 64, or above 65536) decode W with the HIP decoder into a temporary
+    and multiply with torch.matmul on the same device."""
+    s, m, d, e = _streams(sign, mant, delta, emax)
+    out_f, in_f = int(out_f), int(in_f)
+    xx = _dev_tensor(x, "x", tuple(_X_DTYPES))
+    if xx.shape[-1] != in_f:
+        raise ValueError(f"x has last dimension {xx.shape[-1]}, in_f = {in_f}")
+    lead = xx.shape[:-1]
+    x2 = xx.reshape(-1, in_f)
+    if x2.shape[0] == 0:
+        return torch.empty(*lead, out_f, dtype=xx.dtype, device=xx.device)
+    if in_f % 64 != 0 or in_f > 65536:
+        w = bf16x_decode(s, m, d, e, out_f, in_f, sub=sub, plan=plan)
+        y = torch.matmul(x2.float(), w.float().t()) if xx.dtype != torch.bfloat16 else torch.matmul(x2, w.t())
+        return y.to(xx.dtype).reshape(*lead, out_f)
+    if xx.dtype == torch.bfloat16:
+        y = torch.empty(x2.shape[0], out_f, dtype=torch.bfloat16, device=xx.device)
+        _gemm_launch(x2.contiguous(), s, m, d, e, out_f, in_f, plan, y, _lib.BF16, sub)
+    else:
+        xf = x2.float()
+        hi = xf.to(torch.bfloat16)
+        lo = (xf - hi.float()).to(torch.bfloat16)
+        y = torch.empty(x2.shape[0], out_f, dtype=torch.float32, device=xx.device)
+        y2 = torch.empty_like(y)
+        _gemm_launch(hi.contiguous(), s, m, d, e, out_f, in_f, plan, y, _lib.F32, sub)
+        _gemm_launch(lo.contiguous(), s, m, d, e, out_f, in_f, plan, y2, _lib.F32, sub)
+        y = (y + y2).to(xx.dtype)
+    return y.reshape(*lead, out_f)
+
+
+def bf16x_fused_gemm(x, sign, mant, delta, emax, out_f, in_f, group=16, bn=128, bk=32, num_warps=8,
+                     num_stages=1, *, plan: Bf16xPlan | None = None) -> torch.Tensor:
+    """Fused decode+GEMM with the reference's signature (bf16x_gemm_fused.py:97).
+
+    Without `plan` the weight is saturated exactly as the reference kernel
+    decodes it (no overflow correction); with a plan it is exact.  Returns
+    [M, out_f] in x's dtype for x of shape [*, in_f] (M = leading elements).
+    `bn`, `bk`, `num_warps`, `num_stages` are Triton tuning knobs and are
+    ignored; `group` must be 16."""
+    if group != 16:
+        raise _lib.Bf16xError(_lib.ESUB, "bf16x_fused_gemm")
+    y = bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan=plan)
+    return y.reshape(-1, int(out_f))

@@ -143,6 +143,41 @@ int bf16x_gemv(const void* x, int32_t x_dtype,
                int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
                uint16_t* y, bf16x_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Step-major overflow plan for the GEMM (no reference counterpart: the
+ * reference GEMM has no overflow correction, bf16x_gemm_fused.py:9-12).
+ * Built on the device from the row plan (tile_off / tile_ent of
+ * bf16x_plan_host or bf16x_plan_from_csr): entries regrouped by (64-column
+ * step s, 32-row group g).  kp_off: uint32 [bf16x_kplan_size(out_f, in_f)]
+ * = [S*G + 1] with S = in_f/64, G = ceil(out_f/32); kp_ent: uint32
+ * [n_fix], (row & 255) << 22 | (col & 63) << 16 | exact bf16 bits.
+ * Requires in_f % 64 == 0 and in_f <= 65536.  All pointers dev.
+ * ------------------------------------------------------------------------ */
+int64_t bf16x_kplan_size(int64_t out_f, int64_t in_f);
+int bf16x_kplan_build(const uint32_t* tile_off, const uint32_t* tile_ent, int64_t out_f, int64_t in_f,
+                      uint32_t* kp_off, uint32_t* kp_ent, bf16x_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused decode + GEMM (prefill / multi-token).  Replaces bf16x_fused_gemm
+ * (bf16x_gemm_fused.py:97-114) / _bf16x_gemm_fused_kernel (:31-94):
+ * y[M, out_f] = x[M, in_f] . W^T, fp32 accumulation (bf16 MFMA).
+ * mode SATURATED reproduces the reference kernel (code 7 -> emax-7, no
+ * table); EXACT applies the step-major plan (kp_off, kp_ent) for the
+ * lossless weight.  x: dev bf16 [M, in_f], 16-byte aligned; y: dev
+ * [M, out_f] of y_dtype (BF16X_BF16 or BF16X_F32).  Requires in_f % 64 == 0
+ * and in_f <= 65536.  When K is split for parallelism the kernel needs an
+ * fp32 workspace of bf16x_gemm_workspace(M, out_f, in_f) bytes (0 = none);
+ * a smaller one returns BF16X_ECAPACITY.  All pointers dev.
+ * ------------------------------------------------------------------------ */
+int64_t bf16x_gemm_workspace(int64_t M, int64_t out_f, int64_t in_f);
+int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M,
+               const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+               const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+               const uint32_t* kp_off, const uint32_t* kp_ent,
+               int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
+               void* y, int32_t y_dtype, void* workspace, int64_t workspace_bytes,
+               bf16x_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

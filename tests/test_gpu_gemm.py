@@ -1,0 +1,137 @@
+"""GPU parity of the fused decode+GEMM (bf16x_fused_gemm, bf16x_gemm_fused.py:97)
+against the oracle: saturated (the reference kernel's numerics) and exact
+(with the plan), through the C ABI."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import dict_codec as dc
+from tests.test_gpu_dict import DEV, bits_tensor, check_tol, to_dev, with_specials
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def bx():
+    import bfloat16x_amd as m
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return m
+
+
+def _np(d):
+    return {k: (v.numpy() if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+
+
+# (M, out_f, in_f): every tile configuration (M <= 32, <= 64, <= 128, > 128),
+# ragged M and out_f, the C3 prefill shapes at reduced out_f
+CASES = [(1, 128, 64), (5, 96, 128), (16, 512, 4096), (33, 200, 1536), (64, 1024, 4096), (100, 300, 1536),
+         (128, 256, 14336), (256, 1024, 4096), (300, 130, 640), (512, 512, 4096), (2048, 256, 4096)]
+
+
+@pytest.mark.parametrize("M,out_f,in_f", CASES)
+def test_gemm_saturated_and_exact(bx, M, out_f, in_f):
+    print("gemm", M, out_f, in_f, flush=True)
+    bits = with_specials(dc.bench_weight_bits(out_f, in_f, seed=M), seed=3) if out_f * in_f < 1 << 20 else \
+        dc.bench_weight_bits(out_f, in_f, seed=M)
+    bits[(bits & 0x7F00) == 0x7F00] = 0x3F80        # no inf/nan/near-max: keep the products finite
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    dn = _np(d)
+    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+    xn = x.float().numpy()
+    y = bx.bf16x_fused_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f)
+    assert y.dtype == torch.bfloat16 and y.shape == (M, out_f)
+    check_tol(y.float().cpu().numpy(), dc.gemm_ref(dn, xn, saturated=True))
+    plan = bx.build_plan_host(d, device=DEV)
+    ye = bx.bf16x_fused_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                             plan=plan)
+    check_tol(ye.float().cpu().numpy(), dc.gemm_ref(dn, xn, saturated=False))
+
+
+def test_gemm_exact_dense_overflow(bx):
+    """A weight with many overflow entries per row (every atom has several),
+    so the plan window refills inside one atom."""
+    out_f, in_f, M = 64, 1024, 48
+    rng = np.random.default_rng(7)
+    bits = dc.bench_weight_bits(out_f, in_f, seed=7)
+    tiny = rng.random(bits.shape) < 0.3
+    bits[tiny] = (bits[tiny] & 0x807F) | 0x0080              # exponent 1: delta >= 7 next to normal values
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    plan = bx.build_plan_host(d, device=DEV)
+    assert plan.n_fix > out_f * in_f // 32 * 2
+    g = to_dev(d)
+    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
+    y = bx.bf16x_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                      plan=plan)
+    # bit-level check of the weight the kernel used: x = unit rows picks W columns
+    eye = torch.eye(in_f, dtype=torch.bfloat16)[:256]
+    w_cols = bx.bf16x_gemm(eye.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                           plan=plan)
+    assert np.array_equal(w_cols.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).T, bits[:, :256])
+    check_tol(y.float().cpu().numpy(), dc.gemm_ref(_np(d), x.float().numpy(), saturated=False))
+
+
+def test_gemm_identity_is_bit_exact(bx):
+    """x = I: the GEMM returns W^T element for element (one product per output,
+    fp32 accumulate, bf16 store), so the decode inside the GEMM is bit exact."""
+    out_f, in_f = 320, 512
+    bits = dc.bench_weight_bits(out_f, in_f, seed=12)
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    plan = bx.build_plan_host(d, device=DEV)
+    for start in range(0, in_f, 256):
+        eye = torch.zeros(256, in_f, dtype=torch.bfloat16)
+        eye[torch.arange(256), start + torch.arange(256)] = 1
+        for p, ref in ((plan, bits), (None, dc.decode_saturated(_np(d)))):
+            y = bx.bf16x_gemm(eye.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f,
+                              in_f, plan=p)
+            got = y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).T
+            assert np.array_equal(got, ref[:, start:start + 256]), start
+
+
+@pytest.mark.parametrize("xdt", [torch.float16, torch.float32])
+def test_gemm_fp16_fp32_activations(bx, xdt):
+    out_f, in_f, M = 256, 2048, 40
+    bits = dc.bench_weight_bits(out_f, in_f, seed=5)
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    plan = bx.build_plan_host(d, device=DEV)
+    x = torch.randn(2, M // 2, in_f, generator=torch.Generator().manual_seed(6)).to(xdt)
+    y = bx.bf16x_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                      plan=plan)
+    assert y.dtype == xdt and y.shape == (2, M // 2, out_f)
+    y_ref = dc.gemm_ref(_np(d), x.double().numpy().reshape(M, in_f), saturated=False)
+    # fp16 splits exactly into two bf16; fp32 keeps 16 of its 24 mantissa bits
+    # (max 1e-2 / median 2e-3, covers both)
+    tol = dict(max_tol=2e-3, med_tol=5e-4) if xdt == torch.float16 else dict(max_tol=1e-2, med_tol=1e-5)
+    check_tol(y.float().cpu().numpy().reshape(M, out_f), y_ref, **tol)
+
+
+def test_gemm_unfused_shapes(bx):
+    """in_f not a multiple of 64 (and > 65536) goes through decode + matmul."""
+    for out_f, in_f, M in ((40, 96, 7), (3, 70016, 4)):
+        bits = dc.bench_weight_bits(out_f, in_f, seed=in_f)
+        d = bx.bf16x_quantize(bits_tensor(bits))
+        g = to_dev(d)
+        plan = bx.build_plan_host(d, device=DEV)
+        x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
+        y = bx.bf16x_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                          plan=plan)
+        check_tol(y.float().cpu().numpy(), dc.gemm_ref(_np(d), x.float().numpy(), saturated=False))
+
+
+def test_gemm_full_size(bx):
+    """C3 shape 14336x4096 at M = 512, exact: against fp32 matmul of the
+    original weight on the device."""
+    out_f, in_f, M = 14336, 4096, 512
+    print("gemm full", M, out_f, in_f, flush=True)
+    bits = dc.bench_weight_bits(out_f, in_f, seed=0)
+    w = bits_tensor(bits)
+    d = bx.bf16x_quantize(w)
+    g = to_dev(d)
+    plan = bx.build_plan_host(d, device=DEV)
+    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
+    y = bx.bf16x_gemm(x, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f, plan=plan)
+    y_ref = (x.float() @ w.to(DEV).float().t()).double().cpu().numpy()
+    mx, med = check_tol(y.float().cpu().numpy(), y_ref)
+    print("full-size gemm rel err max %.2e median %.2e" % (mx, med), flush=True)
