@@ -39,37 +39,103 @@ __device__ __forceinline__ void apply_plan_rows(const uint32_t* __restrict__ til
 }
 
 // --------------------------------------------------------------------------
-// decode, in_f % 32 == 0: one lane per 32-element atom
+// decode, in_f % 32 == 0: one wave per row, 64 atoms (2048 elements) per pass
 // --------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void decode_atoms_kernel(
+// Lane l decodes atom l of the pass (coalesced stream loads) into a
+// wave-private LDS buffer in natural element order (16-byte chunk q of atom a
+// at slot (q + a/4) & 3, conflict free for both the per-atom writes and the
+// contiguous reads); EXACT then writes the pass's plan entries over it; the
+// buffer is read back so that each store instruction writes 1 KB contiguous.
+// The plan entries of a row segment are sorted by column: the pass's entries
+// are a prefix of the rest of the list, found with a wave ballot.  LDS
+// operations of one wave complete in order, so no barrier is needed.
+__device__ __forceinline__ int chunk_slot(int a, int q) { return a * 64 + (((q + (a >> 2)) & 3) << 4); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dec_rsrc(const void* p, uint64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)n, 0x00020000);
+}
+
+template <bool EXACT>
+__global__ __launch_bounds__(256) void decode_rows_kernel(
     const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta,
     const uint16_t* __restrict__ emax2, const uint32_t* __restrict__ tile_off,
-    const uint32_t* __restrict__ tile_ent, int64_t out_f, int64_t in_f, int tpr, int rows_per_block,
-    uint16_t* __restrict__ out) {
+    const uint32_t* __restrict__ tile_ent, int64_t out_f, int64_t in_f, int tpr, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 4096];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= out_f) return;
+  uint8_t* buf = lds + wave * 4096;
   const int64_t P = in_f >> 5;
-  const int64_t r0 = (int64_t)blockIdx.x * rows_per_block;
-  const int64_t r1 = min(out_f, r0 + rows_per_block);
-  for (int64_t ga = r0 * P + threadIdx.x; ga < r1 * P; ga += blockDim.x) {
-    const Atom t = load_atom(sign, mant, delta, emax2, ga);
+  const int passes = (int)((P + 63) >> 6);
+  // the streams stay below 4 GiB per buffer descriptor: offsets are taken
+  // from the row's first atom
+  const uint64_t a_row = (uint64_t)row * P;
+  const __amdgpu_buffer_rsrc_t rs_ = dec_rsrc(sign + a_row, (uint64_t)P * 4);
+  const __amdgpu_buffer_rsrc_t rm_ = dec_rsrc(mant + a_row * 7, (uint64_t)P * 28);
+  const __amdgpu_buffer_rsrc_t rd_ = dec_rsrc(delta + a_row * 3, (uint64_t)P * 12);
+  const __amdgpu_buffer_rsrc_t re_ = dec_rsrc(emax2 + a_row, (uint64_t)P * 2);
+  auto load = [&](int c, Atom& t) {
+    const uint32_t a = (uint32_t)min((int64_t)c * 64 + lane, P - 1);
+    const u32x4 m03 = __builtin_amdgcn_raw_buffer_load_b128(rm_, (int)(a * 28), 0, 0);
+    const u32x3 m46 = __builtin_amdgcn_raw_buffer_load_b96(rm_, (int)(a * 28 + 16), 0, 0);
+    const u32x3 d02 = __builtin_amdgcn_raw_buffer_load_b96(rd_, (int)(a * 12), 0, 0);
+    t.s = __builtin_amdgcn_raw_buffer_load_b32(rs_, (int)(a * 4), 0, 0);
+    t.e = __builtin_amdgcn_raw_buffer_load_b16(re_, (int)(a * 2), 0, 0);
+    const uint32_t c0 = m03.x, c1 = m03.y, c2 = m03.z, c3 = m03.w, c4 = m46.x, c5 = m46.y, c6 = m46.z;
+    t.m[0] = c0; t.m[1] = c1; t.m[2] = c2; t.m[3] = c3; t.m[4] = c4; t.m[5] = c5; t.m[6] = c6;
+    const uint32_t e0 = d02.x, e1 = d02.y, e2 = d02.z;
+    t.d[0] = e0; t.d[1] = e1; t.d[2] = e2;
+  };
+  uint16_t* orow = out + row * in_f;
+  uint32_t ptr = 0, pend = 0;                   // plan entries of the current segment
+  Atom cur, nxt;
+  load(0, cur);
+  for (int c = 0; c < passes; ++c) {
+    if (c + 1 < passes) load(c + 1, nxt);
     uint32_t p[16];
-    decode_pairs(t, p);
+    decode_pairs(cur, p);
     uint32_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       lo[i] = perm(p[2 * i + 1], p[2 * i], 0x05040100u);  // elements 2i, 2i+1
       hi[i] = perm(p[2 * i + 1], p[2 * i], 0x07060302u);  // elements 16+2i, 17+2i
     }
-    u32x4a* o = (u32x4a*)(out + 32 * ga);
-    o[0] = u32x4a{lo[0], lo[1], lo[2], lo[3]};
-    o[1] = u32x4a{lo[4], lo[5], lo[6], lo[7]};
-    o[2] = u32x4a{hi[0], hi[1], hi[2], hi[3]};
-    o[3] = u32x4a{hi[4], hi[5], hi[6], hi[7]};
-  }
-  if (tile_off != nullptr) {
-    // every saturated store of the block completes before any exact store
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    apply_plan_rows(tile_off, tile_ent, r0, r1, in_f, tpr, out);
+    *(u32x4*)(buf + chunk_slot(lane, 0)) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    *(u32x4*)(buf + chunk_slot(lane, 1)) = u32x4{lo[4], lo[5], lo[6], lo[7]};
+    *(u32x4*)(buf + chunk_slot(lane, 2)) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    *(u32x4*)(buf + chunk_slot(lane, 3)) = u32x4{hi[4], hi[5], hi[6], hi[7]};
+    const int64_t col0 = (int64_t)c * 2048;
+    if constexpr (EXACT) {
+      const int64_t seg = col0 / kTileCols;
+      const uint32_t cs = (uint32_t)(col0 - seg * kTileCols);   // pass start within the segment
+      if (cs == 0) {
+        ptr = tile_off[row * tpr + seg];
+        pend = tile_off[row * tpr + seg + 1];
+      }
+      while (true) {
+        const uint32_t idx = ptr + lane;
+        const uint32_t ent = idx < pend ? tile_ent[idx] : 0xFFFFFFFFu;
+        const uint32_t col = ent >> 16;
+        const bool in = idx < pend && col < cs + 2048;
+        if (in) {
+          const int e = (int)(col - cs);
+          *(uint16_t*)(buf + chunk_slot(e >> 5, (e & 31) >> 3) + (e & 7) * 2) = (uint16_t)(ent & 0xFFFFu);
+        }
+        const uint32_t cnt = (uint32_t)__builtin_popcountll(__ballot(in));
+        ptr += cnt;
+        if (cnt < 64) break;
+      }
+    }
+    const int64_t nvalid = min((int64_t)2048, in_f - col0);        // elements of this pass
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 8 * lane + 512 * i;
+      const u32x4 v = *(const u32x4*)(buf + chunk_slot(e >> 5, (e & 31) >> 3));
+      if (e < nvalid) *(u32x4a*)(orow + col0 + e) = v;
+    }
+    cur = nxt;
   }
 }
 
@@ -146,15 +212,17 @@ extern "C" int bf16x_decode(const int32_t* sign, int64_t n_sign, const int32_t* 
   const int tpr = tiles_per_row(in_f);
   hipStream_t st = (hipStream_t)stream;
   if ((in_f & 31) == 0 && aligned4(sign) && aligned4(mant) && aligned4(delta) && aligned2(emax) &&
-      aligned4(out)) {
-    const int64_t P = in_f >> 5;
-    int64_t rpb = std::max<int64_t>(1, 1024 / P);
-    while (rpb > 1 && (out_f + rpb - 1) / rpb < 1024) rpb >>= 1;
-    const int64_t grid = (out_f + rpb - 1) / rpb;
+      aligned16(out) && (in_f >> 5) * 28 < (int64_t)0xFFFFFFFF) {
+    const int64_t grid = (out_f + 3) / 4;      // one wave per row
     if (grid > INT32_MAX) return BF16X_ESHAPE;
-    hipLaunchKernelGGL(decode_atoms_kernel, dim3((unsigned)grid), dim3(256), 0, st, (const uint32_t*)sign,
-                       (const uint32_t*)mant, (const uint32_t*)delta, (const uint16_t*)emax, to, tile_ent,
-                       out_f, in_f, tpr, (int)rpb, out);
+    if (to)
+      hipLaunchKernelGGL(decode_rows_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, (const uint32_t*)sign,
+                         (const uint32_t*)mant, (const uint32_t*)delta, (const uint16_t*)emax, to, tile_ent,
+                         out_f, in_f, tpr, out);
+    else
+      hipLaunchKernelGGL(decode_rows_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, (const uint32_t*)sign,
+                         (const uint32_t*)mant, (const uint32_t*)delta, (const uint16_t*)emax, to, tile_ent,
+                         out_f, in_f, tpr, out);
   } else {
     int64_t rpb = std::max<int64_t>(1, 8192 / in_f);
     while (rpb > 1 && (out_f + rpb - 1) / rpb < 1024) rpb >>= 1;

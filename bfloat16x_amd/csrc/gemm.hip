@@ -75,7 +75,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   static_assert(BN == kBN, "one atom per thread per step");
   constexpr int X_BYTES = BM * kRowBytes;
   constexpr int W_BYTES = BN * kRowBytes;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * X_BYTES + 3 * W_BYTES];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * X_BYTES + 3 * W_BYTES + 512];   // + patch trash slots
+  uint8_t* const trash = lds + 2 * X_BYTES + 3 * W_BYTES;
   uint8_t* const wbase = lds + 2 * X_BYTES;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -174,15 +175,19 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     r.e0 = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((r.beg + tid) * 4), 0, 0);
     r.e1 = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((r.beg + tid + 256) * 4), 0, 0);
   };
-  auto patch_one = [&](uint32_t e, uint8_t* wb) {
+  // Entries past the run's end go to this thread's trash slot: the store is
+  // unconditional, so the entry is not first used under a divergent branch
+  // (which would make the compiler wait for every outstanding load).
+  auto patch_one = [&](uint32_t e, uint8_t* wb, bool live) {
     const int r = (int)(e >> 22) & (BN - 1), c = (int)(e >> 16) & 63;
-    *(uint16_t*)(wb + r * kRowBytes + swz(r, c >> 3) * 16 + (c & 7) * 2) = (uint16_t)(e & 0xFFFFu);
+    uint8_t* dst = live ? wb + r * kRowBytes + swz(r, c >> 3) * 16 + (c & 7) * 2 : trash + 2 * tid;
+    *(uint16_t*)dst = (uint16_t)(e & 0xFFFFu);
   };
   auto apply_run = [&](const Run& r, uint8_t* wb) {
-    if (r.beg + tid < r.end) patch_one(r.e0, wb);
-    if (r.beg + tid + 256 < r.end) patch_one(r.e1, wb);
+    patch_one(r.e0, wb, r.beg + tid < r.end);
+    patch_one(r.e1, wb, r.beg + tid + 256 < r.end);
     for (uint32_t e = r.beg + 512 + tid; e < r.end; e += 256)   // dense runs (rare)
-      patch_one(kp_ent[e], wb);
+      patch_one(kp_ent[e], wb, true);
   };
 
   // ---- x tile: 16-byte chunk c = i*256 + tid of the step's BM x 64 tile is
@@ -445,7 +450,20 @@ extern "C" int bf16x_kplan_build(const uint32_t* tile_off, const uint32_t* tile_
   return launch_status();
 }
 
+// few-row kernel (gemm_skinny.hip): M <= skinny_rows()
+int bf16x_gemm_skinny_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m, const uint32_t* d,
+                             const uint16_t* e, const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f,
+                             int64_t in_f, bool exact, bool yf32, void* y, hipStream_t st);
+
 namespace {
+
+// Largest M served by the few-row kernel (at most 128, its column-block
+// limit; measured faster than the tiled kernel up to 32 rows).
+int64_t skinny_rows() {
+  int64_t r = 32;
+  if (const char* e = getenv("BF16X_GEMM_SKINNY_MAX")) r = atoll(e);
+  return r < 0 ? 0 : (r > 128 ? 128 : r);
+}
 
 struct GemmShape {
   int bm;        // rows of x per tile
@@ -455,8 +473,9 @@ struct GemmShape {
 
 // Tile height and K split.  BM = 256 above 128 rows (W decoded once per 256
 // rows of x).  Then K is split while the tile count leaves CUs idle: the split
-// minimises (rounds of resident blocks) x (steps per block), with a small
-// charge per extra split for the partials, smallest split on ties.
+// minimises (rounds of resident blocks) x (steps per block), with a charge of
+// 15% per extra split (fp32 partials written and summed, per-block prologue),
+// smallest split on ties.
 GemmShape gemm_shape(int64_t M, int64_t out_f, int64_t in_f) {
   GemmShape g;
   g.bm = M <= 32 ? 32 : M <= 64 ? 64 : M <= 128 ? 128 : 256;
@@ -468,7 +487,7 @@ GemmShape gemm_shape(int64_t M, int64_t out_f, int64_t in_f) {
   double best_cost = 1e30;
   for (int k = 1; k <= 32 && k * 4 <= S; ++k) {
     const int64_t sps = (S + k - 1) / k, ks = (S + sps - 1) / sps;
-    const double cost = (double)((tiles * ks + slots - 1) / slots) * sps * (1.0 + 0.02 * (ks - 1));
+    const double cost = (double)((tiles * ks + slots - 1) / slots) * sps * (1.0 + 0.15 * (ks - 1));
     if (cost < best_cost - 1e-9) { best_cost = cost; best = (int)ks; }
   }
   if (const char* e = getenv("BF16X_GEMM_SPLIT")) best = atoi(e);
@@ -481,7 +500,7 @@ GemmShape gemm_shape(int64_t M, int64_t out_f, int64_t in_f) {
 }  // namespace
 
 extern "C" int64_t bf16x_gemm_workspace(int64_t M, int64_t out_f, int64_t in_f) {
-  if (M <= 0 || out_f <= 0 || in_f < kBK) return 0;
+  if (M <= 0 || out_f <= 0 || in_f < kBK || M <= skinny_rows()) return 0;
   const GemmShape g = gemm_shape(M, out_f, in_f);
   return g.nsplit > 1 ? (int64_t)g.nsplit * M * out_f * 4 : 0;
 }
@@ -503,6 +522,13 @@ extern "C" int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M, const int32
   if (out_f * (in_f >> 5) * 28 >= (int64_t)0xFFFFFFFF || M * in_f * 2 >= (int64_t)0xFFFFFFFF) return BF16X_ESHAPE;
   if (!aligned4(sign) || !aligned4(mant) || !aligned4(delta) || !aligned2(emax) || !aligned16(x) || !aligned4(y))
     return BF16X_EARG;
+  hipStream_t st = (hipStream_t)stream;
+  if (M <= skinny_rows()) {
+    rc = bf16x_gemm_skinny_launch((const uint16_t*)x, M, (const uint32_t*)sign, (const uint32_t*)mant,
+                                  (const uint32_t*)delta, (const uint16_t*)emax, kp_off, kp_ent, out_f, in_f,
+                                  mode == BF16X_EXACT, y_dtype == BF16X_F32, y, st);
+    return rc ? rc : launch_status();
+  }
   const GemmShape g = gemm_shape(M, out_f, in_f);
   if (g.bm != 32 && g.bm != 64 && g.bm != 128 && g.bm != 256) return BF16X_EARG;
   const bool split = g.nsplit > 1;
@@ -510,7 +536,6 @@ extern "C" int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M, const int32
     return BF16X_ECAPACITY;
   const int64_t grid = ((M + g.bm - 1) / g.bm) * ((out_f + kBN - 1) / kBN) * g.nsplit;
   if (grid > INT32_MAX) return BF16X_ESHAPE;
-  hipStream_t st = (hipStream_t)stream;
   const bool exact = mode == BF16X_EXACT, yf = y_dtype == BF16X_F32;
   const uint16_t* xb = (const uint16_t*)x;
   const uint32_t* s = (const uint32_t*)sign;

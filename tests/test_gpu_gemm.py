@@ -135,3 +135,27 @@ def test_gemm_full_size(bx):
     y_ref = (x.float() @ w.to(DEV).float().t()).double().cpu().numpy()
     mx, med = check_tol(y.float().cpu().numpy(), y_ref)
     print("full-size gemm rel err max %.2e median %.2e" % (mx, med), flush=True)
+
+
+@pytest.mark.parametrize("M", [32, 64, 100])
+def test_gemm_few_rows_identity_is_bit_exact(bx, M):
+    """The few-row kernel (M <= 128): x = rows of I select W columns, so the
+    decode that feeds its MFMA is checked bit for bit, exact and saturated."""
+    out_f, in_f = 96, 1024
+    bits = with_specials(dc.bench_weight_bits(out_f, in_f, seed=M), seed=M)
+    bits[(bits & 0x7F00) == 0x7F00] = 0x3F80
+    bits[(bits & 0x7F80) == 0] = 0                       # MFMA inputs: no subnormals
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    plan = bx.build_plan_host(d, device=DEV)
+    sat = dc.decode_saturated(_np(d))
+    sat[(sat & 0x7F80) == 0] = 0
+    for start in range(0, in_f, M):
+        cols = min(M, in_f - start)
+        eye = torch.zeros(M, in_f, dtype=torch.bfloat16)
+        eye[torch.arange(cols), start + torch.arange(cols)] = 1
+        for p, ref in ((plan, bits), (None, sat)):
+            y = bx.bf16x_gemm(eye.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f,
+                              in_f, plan=p)
+            got = y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)[:cols].T
+            assert np.array_equal(got, ref[:, start:start + cols]), (start, p is None)
