@@ -12,6 +12,11 @@ streams its weight from HBM.  Inputs are resident in HBM before timing.
 value = algorithmic bytes per launch / mean launch time (HIP events on the
 launch stream), where algorithmic bytes =
 4*(|sign|+|mant|+|delta|) + |emax| + 5*n_fix + 2*in_f + 2*out_f.
+Secondary fields (same rotation): the exact decode kernel's time and
+read+write bandwidth, and decode+GEMM (configuration 3) at --gemm-rows
+activation rows through the fused kernel ("fused") and the default dispatch
+("auto": fused below 256 rows, decode + hipBLASLt from 256 rows on), with
+torch bf16 F.linear on the decoded weight beside them.
 Printed as one JSON line; diagnostics go to stderr.
 """
 from __future__ import annotations
@@ -101,6 +106,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=7168)
+    ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 2048],
+                    help="activation rows of the decode+GEMM lines (configuration 3)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -166,6 +173,43 @@ def main():
     log(f"bf16 F.linear gemv: {sec_bf16 * 1e6:.2f} us ({wd.numel() * 2 / sec_bf16 / 1e9:.1f} GB/s of bf16 bytes)")
     del wcopies
 
+    # ---- decode (exact) and decode+GEMM at the configuration-3 shape, same rotation
+    dec_out = torch.empty(out_f, in_f, dtype=torch.bfloat16, device=dev)
+
+    def step_dec(i):
+        g, p = copies[i % n_copies]
+        bx.bf16x_decode(g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f, plan=p,
+                        out=dec_out)
+
+    sec_dec = time_launches(step_dec, 60, 6, stream)
+    dec_bytes = comp_bytes + 2 * out_f * in_f
+    decode_rec = {"us": round(sec_dec * 1e6, 2), "GBps_read_plus_write": round(dec_bytes / sec_dec / 1e9, 1),
+                  "hbm_frac": round(dec_bytes / sec_dec / 1e9 / HBM_PEAK_GBS, 4)}
+    log(f"decode exact: {decode_rec}")
+    del dec_out
+    gemm_rec = []
+    for _, p in copies:
+        p.kplan()                      # step-major plans built once, outside the timed region
+    for M in args.gemm_rows:
+        xm = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16).to(dev)
+        flops = 2.0 * M * out_f * in_f
+        ent = {"M": M}
+        for path in ("fused", "auto"):
+            def step_g(i, path=path):
+                g, p = copies[i % n_copies]
+                bx.bf16x_gemm(xm, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                              plan=p, path=path)
+            n_l = max(6, min(60, int(0.05 / max(flops / 5e14, 1e-6))))
+            sec_g = time_launches(step_g, n_l, 3, stream)
+            ent[f"{path}_us"] = round(sec_g * 1e6, 2)
+            ent[f"{path}_tflops"] = round(flops / sec_g / 1e12, 1)
+        sec_t = time_launches(lambda i: torch.nn.functional.linear(xm, wd), 30, 3, stream)
+        ent["torch_bf16_linear_us"] = round(sec_t * 1e6, 2)
+        ent["auto_mfma_frac"] = round(flops / (ent["auto_us"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+        gemm_rec.append(ent)
+        log(f"gemm {ent}")
+        del xm
+
     cpu = None
     if not args.no_cpu:
         t = time.time()
@@ -194,6 +238,8 @@ def main():
         "bf16_gemv_us": round(sec_bf16 * 1e6, 3),
         "speedup_vs_bf16_gemv": round(sec_bf16 / sec, 3),
         "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "decode_exact_14336x4096": decode_rec,
+        "gemm_14336x4096_exact": gemm_rec,
     }
     print(json.dumps(rec), flush=True)
 

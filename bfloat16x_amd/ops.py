@@ -11,6 +11,7 @@ a missing library or a CPU tensor raises.
 from __future__ import annotations
 
 import collections
+import os
 
 import torch
 
@@ -166,15 +167,30 @@ def _gemm_launch(x2, s, m, d, e, out_f, in_f, plan, y, y_dtype, sub=16):
     _lib.check(st, "bf16x_gemm")
 
 
-def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None = None, sub=16) -> torch.Tensor:
-    """y[..., out_f] = x[..., in_f] . W^T with W decoded on the fly, in x's dtype.
+# From this many activation rows on, bf16x_gemm decodes W once at HBM speed
+# and runs the product as a plain library GEMM (hipBLASLt through
+# F.linear): the decode is amortised over the rows and the library GEMM runs
+# closer to the MFMA peak than the fused kernel.  Below it the fused kernel
+# avoids writing the decoded weight.
+GEMM_DECODE_MIN_ROWS = int(os.environ.get("BF16X_GEMM_DECODE_MIN_ROWS", "256"))
 
-    Exact with a plan, saturated without one.  bf16 activations run one bf16
-    MFMA pass; fp16/fp32 activations are split as x = hi + lo (two bf16
-    tensors, exact for fp16, 16 mantissa bits for fp32) and accumulated over
-    two passes in fp32.  Shapes outside the fused kernel (in_f not a multiple
-    of 64, or above 65536) decode W with the HIP decoder into a temporary
-    and multiply with torch.matmul on the same device."""
+
+def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None = None, sub=16,
+               path: str = "auto") -> torch.Tensor:
+    """y[..., out_f] = x[..., in_f] . W^T, in x's dtype.  Exact with a plan,
+    saturated without one.
+
+    path "fused": the fused decode+GEMM kernel (bf16x_gemm in the C ABI);
+    bf16 activations run one bf16 MFMA pass, fp16/fp32 activations are split
+    as x = hi + lo (two bf16 tensors, exact for fp16, 16 mantissa bits for
+    fp32) accumulated over two passes in fp32.
+    path "decode": W decoded into a temporary by the HIP decoder, then
+    F.linear on the same device (fp32 for fp16/fp32 activations).
+    path "auto": "decode" from GEMM_DECODE_MIN_ROWS rows on and for shapes the
+    fused kernel does not take (in_f not a multiple of 64, or above 65536),
+    "fused" otherwise."""
+    if path not in ("auto", "fused", "decode"):
+        raise ValueError(f"path must be auto, fused or decode, not {path!r}")
     s, m, d, e = _streams(sign, mant, delta, emax)
     out_f, in_f = int(out_f), int(in_f)
     xx = _dev_tensor(x, "x", tuple(_X_DTYPES))
@@ -184,9 +200,15 @@ def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None =
     x2 = xx.reshape(-1, in_f)
     if x2.shape[0] == 0:
         return torch.empty(*lead, out_f, dtype=xx.dtype, device=xx.device)
-    if in_f % 64 != 0 or in_f > 65536:
+    fusable = in_f % 64 == 0 and in_f <= 65536
+    if path == "fused" and not fusable:
+        raise _lib.Bf16xError(_lib.ESHAPE, "bf16x_gemm (fused path needs in_f % 64 == 0 and in_f <= 65536)")
+    if path == "decode" or (path == "auto" and (not fusable or x2.shape[0] >= GEMM_DECODE_MIN_ROWS)):
         w = bf16x_decode(s, m, d, e, out_f, in_f, sub=sub, plan=plan)
-        y = torch.matmul(x2.float(), w.float().t()) if xx.dtype != torch.bfloat16 else torch.matmul(x2, w.t())
+        if xx.dtype == torch.bfloat16:
+            y = torch.nn.functional.linear(x2.contiguous(), w)
+        else:
+            y = torch.nn.functional.linear(x2.float(), w.float())
         return y.to(xx.dtype).reshape(*lead, out_f)
     if xx.dtype == torch.bfloat16:
         y = torch.empty(x2.shape[0], out_f, dtype=torch.bfloat16, device=xx.device)
@@ -204,7 +226,7 @@ def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None =
 
 
 def bf16x_fused_gemm(x, sign, mant, delta, emax, out_f, in_f, group=16, bn=128, bk=32, num_warps=8,
-                     num_stages=1, *, plan: Bf16xPlan | None = None) -> torch.Tensor:
+                     num_stages=1, *, plan: Bf16xPlan | None = None, path: str = "auto") -> torch.Tensor:
     """Fused decode+GEMM with the reference's signature (bf16x_gemm_fused.py:97).
 
     Without `plan` the weight is saturated exactly as the reference kernel
@@ -214,5 +236,5 @@ def bf16x_fused_gemm(x, sign, mant, delta, emax, out_f, in_f, group=16, bn=128, 
     ignored; `group` must be 16."""
     if group != 16:
         raise _lib.Bf16xError(_lib.ESUB, "bf16x_fused_gemm")
-    y = bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan=plan)
+    y = bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan=plan, path=path)
     return y.reshape(-1, int(out_f))

@@ -28,9 +28,10 @@ CASES = [(1, 128, 64), (5, 96, 128), (16, 512, 4096), (33, 200, 1536), (64, 1024
          (128, 256, 14336), (256, 1024, 4096), (300, 130, 640), (512, 512, 4096), (2048, 256, 4096)]
 
 
+@pytest.mark.parametrize("path", ["fused", "auto"])
 @pytest.mark.parametrize("M,out_f,in_f", CASES)
-def test_gemm_saturated_and_exact(bx, M, out_f, in_f):
-    print("gemm", M, out_f, in_f, flush=True)
+def test_gemm_saturated_and_exact(bx, M, out_f, in_f, path):
+    print("gemm", M, out_f, in_f, path, flush=True)
     bits = with_specials(dc.bench_weight_bits(out_f, in_f, seed=M), seed=3) if out_f * in_f < 1 << 20 else \
         dc.bench_weight_bits(out_f, in_f, seed=M)
     bits[(bits & 0x7F00) == 0x7F00] = 0x3F80        # no inf/nan/near-max: keep the products finite
@@ -39,12 +40,13 @@ def test_gemm_saturated_and_exact(bx, M, out_f, in_f):
     dn = _np(d)
     x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
     xn = x.float().numpy()
-    y = bx.bf16x_fused_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f)
+    y = bx.bf16x_fused_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                            path=path)
     assert y.dtype == torch.bfloat16 and y.shape == (M, out_f)
     check_tol(y.float().cpu().numpy(), dc.gemm_ref(dn, xn, saturated=True))
     plan = bx.build_plan_host(d, device=DEV)
     ye = bx.bf16x_fused_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
-                             plan=plan)
+                             plan=plan, path=path)
     check_tol(ye.float().cpu().numpy(), dc.gemm_ref(dn, xn, saturated=False))
 
 
@@ -62,11 +64,11 @@ def test_gemm_exact_dense_overflow(bx):
     g = to_dev(d)
     x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16)
     y = bx.bf16x_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
-                      plan=plan)
+                      plan=plan, path="fused")
     # bit-level check of the weight the kernel used: x = unit rows picks W columns
     eye = torch.eye(in_f, dtype=torch.bfloat16)[:256]
     w_cols = bx.bf16x_gemm(eye.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
-                           plan=plan)
+                           plan=plan, path="fused")
     assert np.array_equal(w_cols.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).T, bits[:, :256])
     check_tol(y.float().cpu().numpy(), dc.gemm_ref(_np(d), x.float().numpy(), saturated=False))
 
@@ -84,7 +86,7 @@ def test_gemm_identity_is_bit_exact(bx):
         eye[torch.arange(256), start + torch.arange(256)] = 1
         for p, ref in ((plan, bits), (None, dc.decode_saturated(_np(d)))):
             y = bx.bf16x_gemm(eye.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f,
-                              in_f, plan=p)
+                              in_f, plan=p, path="fused")
             got = y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16).T
             assert np.array_equal(got, ref[:, start:start + 256]), start
 
@@ -98,7 +100,7 @@ def test_gemm_fp16_fp32_activations(bx, xdt):
     plan = bx.build_plan_host(d, device=DEV)
     x = torch.randn(2, M // 2, in_f, generator=torch.Generator().manual_seed(6)).to(xdt)
     y = bx.bf16x_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
-                      plan=plan)
+                      plan=plan, path="fused")
     assert y.dtype == xdt and y.shape == (2, M // 2, out_f)
     y_ref = dc.gemm_ref(_np(d), x.double().numpy().reshape(M, in_f), saturated=False)
     # fp16 splits exactly into two bf16; fp32 keeps 16 of its 24 mantissa bits
@@ -131,10 +133,12 @@ def test_gemm_full_size(bx):
     g = to_dev(d)
     plan = bx.build_plan_host(d, device=DEV)
     x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(DEV)
-    y = bx.bf16x_gemm(x, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f, plan=plan)
     y_ref = (x.float() @ w.to(DEV).float().t()).double().cpu().numpy()
-    mx, med = check_tol(y.float().cpu().numpy(), y_ref)
-    print("full-size gemm rel err max %.2e median %.2e" % (mx, med), flush=True)
+    for path in ("fused", "auto"):
+        y = bx.bf16x_gemm(x, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f, plan=plan,
+                          path=path)
+        mx, med = check_tol(y.float().cpu().numpy(), y_ref)
+        print("full-size gemm (%s) rel err max %.2e median %.2e" % (path, mx, med), flush=True)
 
 
 @pytest.mark.parametrize("M", [32, 64, 100])
@@ -156,6 +160,6 @@ def test_gemm_few_rows_identity_is_bit_exact(bx, M):
         eye[torch.arange(cols), start + torch.arange(cols)] = 1
         for p, ref in ((plan, bits), (None, sat)):
             y = bx.bf16x_gemm(eye.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f,
-                              in_f, plan=p)
+                              in_f, plan=p, path="fused")
             got = y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)[:cols].T
             assert np.array_equal(got, ref[:, start:start + cols]), (start, p is None)
