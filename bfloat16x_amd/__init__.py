@@ -5,16 +5,19 @@ Call surface (mirrors the reference dfytensor/bfloat16x):
   bf16x_decode / bf16x_decode_triton   bf16x_triton_test.py:80
   bf16x_fused_gemv                     bf16x_fused.py:114
   bf16x_fused_gemm                     bf16x_gemm_fused.py:97
+  gguf.quantize_blocks / dequantize_blocks / quantize_tensor / fp32_to_bf16_bits
+                                       bf16x_gguf_block.py:44-93
 All GPU work runs in the HIP library libbf16x_hip.so through its C ABI
 (include/bf16x_hip.h).
 """
 from ._lib import Bf16xError, version
 from .codec import Bf16xPlan, bf16x_quantize, build_plan_host, stream_words
+from . import gguf
 from .ops import (bf16x_decode, bf16x_decode_triton, bf16x_fused_gemm, bf16x_fused_gemv, bf16x_gemm,
                   bf16x_gemv)
 
 __all__ = [
     "Bf16xError", "Bf16xPlan", "bf16x_decode", "bf16x_decode_triton", "bf16x_fused_gemm", "bf16x_fused_gemv",
     "bf16x_gemm", "bf16x_gemv",
-    "bf16x_quantize", "build_plan_host", "stream_words", "version",
+    "bf16x_quantize", "build_plan_host", "gguf", "stream_words", "version",
 ]

@@ -89,9 +89,39 @@ __device__ __forceinline__ Atom load_atom(const uint32_t* __restrict__ sign,
   return t;
 }
 
+// per-16-bit-lane a - b modulo 2^16 (v_pk_sub_u16)
+__device__ __forceinline__ uint32_t pk_sub_wrap(uint32_t a, uint32_t b) {
+  u16x2 x, y;
+  __builtin_memcpy(&x, &a, 4);
+  __builtin_memcpy(&y, &b, 4);
+  u16x2 r = x - y;
+  uint32_t o;
+  __builtin_memcpy(&o, &r, 4);
+  return o;
+}
+// per-16-bit-lane arithmetic shift right by 15: 0xFFFF where bit 15 is set
+__device__ __forceinline__ uint32_t pk_ashr15(uint32_t a) {
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  s16x2 x;
+  __builtin_memcpy(&x, &a, 4);
+  s16x2 r = x >> (short)15;
+  uint32_t o;
+  __builtin_memcpy(&o, &r, 4);
+  return o;
+}
+// (m & a) | (~m & b): v_bfi_b32
+__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) { return (m & a) | (~m & b); }
+
 // Decode an atom into 16 packed pairs: out[j] = bf16(elem j) | bf16(elem j+16) << 16.
-// SAT: the 3-bit code is used as the delta (code 7 -> exponent emax-7); the
-// exponent is clamped at 0 like the reference kernels (bf16x_triton_test.py:50).
+// ZERO7 = false (packed dict): the 3-bit code is the exponent delta, code 7
+// saturating at emax-7; the exponent is clamped at 0 like the reference
+// kernels (bf16x_triton_test.py:50).
+// ZERO7 = true (GGUF half-block, bf16x_gguf_block.py:76-87): code 7 is a zero
+// marker (exponent 0), and emax - code is formed in uint16 as there, so a
+// malformed block with emax < code wraps instead of clamping.  Per lane,
+// (code << 12) + 0x1000 reaches bit 15 exactly for code 7; an arithmetic
+// shift by 15 widens that bit to a lane mask which clears the exponent.
+template <bool ZERO7 = false>
 __device__ __forceinline__ void decode_pairs(const Atom& t, uint32_t out[16]) {
   // 16-bit-lane transposition: lane lo = elements 0..15, lane hi = 16..31
   uint32_t pm[7];
@@ -130,7 +160,13 @@ __device__ __forceinline__ void decode_pairs(const Atom& t, uint32_t out[16]) {
       dsh = perm(pd[dk + 1], pd[dk], 0x06030401u) << (15 - dof);
     }
     dsh &= 0x03800380u;
-    const uint32_t ex = pk_sub_sat(E, dsh);                 // (emax - d) << 7 per lane
+    uint32_t ex;
+    if constexpr (ZERO7) {
+      const uint32_t t15 = (dsh << 5) + 0x10001000u;         // bit 15 of a lane set iff code == 7
+      ex = bfi(pk_ashr15(t15), 0u, pk_sub_wrap(E, dsh));      // (emax - d) << 7 mod 2^16, 0 for code 7
+    } else {
+      ex = pk_sub_sat(E, dsh);                               // (emax - d) << 7 per lane, clamped at 0
+    }
     const uint32_t ssh = (j == 15) ? t.s : (t.s << (15 - j));
     // v_bitop3 0xEA = (S0 & S1) | S2: mantissa bits into the exponent word,
     // then the two sign bits (ex has zeros at both masks' positions)
@@ -145,6 +181,47 @@ __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
   uint32_t u = __float_as_uint(f);
   if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x0040u) & 0xFFFFu;
   return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// GGUF half-block (bf16x_gguf_block.py:6-17): block b is 46 bytes at 46*b,
+// [emax lo, emax hi | sign 4 | mant 28 | delta 12], the dict atom's fields in
+// AoS order.  Blocks are 2-byte aligned: the 48 bytes from the dword at or
+// below the block are loaded (three 16-byte loads, dword aligned) and
+// shifted by 0 or 16 bits.  The shift is done where the block is decoded, not
+// where it is loaded (values computed from a load at the load site make the
+// compiler wait for it there).  `rs` must cover the buffer rounded up to a
+// multiple of 4 bytes.
+struct GgufRaw {
+  u32x4 q0, q1, q2;
+  uint32_t sh;                     // 0 or 16
+};
+
+__device__ __forceinline__ void load_gguf_raw(__amdgpu_buffer_rsrc_t rs, uint32_t boff, GgufRaw& r) {
+  const uint32_t base = boff & ~3u;
+  r.sh = (boff & 2u) * 8u;
+  r.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)base, 0, 0);
+  r.q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(base + 16), 0, 0);
+  r.q2 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(base + 32), 0, 0);
+}
+
+__device__ __forceinline__ Atom gguf_atom(const GgufRaw& r) {
+  const uint32_t sh = r.sh;
+  const uint32_t w0 = r.q0.x, w1 = r.q0.y, w2 = r.q0.z, w3 = r.q0.w, w4 = r.q1.x, w5 = r.q1.y, w6 = r.q1.z;
+  const uint32_t w7 = r.q1.w, w8 = r.q2.x, w9 = r.q2.y, w10 = r.q2.z, w11 = r.q2.w;
+  // block word k (bytes 4k..4k+3 of the block) = alignbit(w[k+1], w[k], sh);
+  // word 11 only needs its low half (block bytes 44-45)
+  const uint32_t b0 = alignbit(w1, w0, sh), b1 = alignbit(w2, w1, sh), b2 = alignbit(w3, w2, sh);
+  const uint32_t b3 = alignbit(w4, w3, sh), b4 = alignbit(w5, w4, sh), b5 = alignbit(w6, w5, sh);
+  const uint32_t b6 = alignbit(w7, w6, sh), b7 = alignbit(w8, w7, sh), b8 = alignbit(w9, w8, sh);
+  const uint32_t b9 = alignbit(w10, w9, sh), b10 = alignbit(w11, w10, sh), b11 = alignbit(w11, w11, sh);
+  Atom t;
+  t.e = (uint16_t)b0;                                         // bytes 0-1
+  t.s = alignbit(b1, b0, 16);                                 // bytes 2-5
+  t.m[0] = alignbit(b2, b1, 16); t.m[1] = alignbit(b3, b2, 16); t.m[2] = alignbit(b4, b3, 16);
+  t.m[3] = alignbit(b5, b4, 16); t.m[4] = alignbit(b6, b5, 16); t.m[5] = alignbit(b7, b6, 16);
+  t.m[6] = alignbit(b8, b7, 16);                              // bytes 6-33
+  t.d[0] = alignbit(b9, b8, 16); t.d[1] = alignbit(b10, b9, 16); t.d[2] = alignbit(b11, b10, 16);  // 34-45
+  return t;
 }
 
 __device__ __forceinline__ float bf16lo_to_f32(uint32_t p) { return __uint_as_float(p << 16); }

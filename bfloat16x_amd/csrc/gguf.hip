@@ -1,0 +1,225 @@
+// GGUF half-block BF16X (bf16x_gguf_block.py:6-17, 25-93) on gfx950: decode
+// and decode+GEMV.
+//
+// A weight [out_f, in_f] (in_f % 32 == 0) is out_f * in_f / 32 blocks of 46
+// bytes in row-major order; block b holds the 32 elements 32b .. 32b+31.
+// Decoding follows bf16x_gguf_block.py:76-87: exponent = 0 if code == 7
+// (zero marker) else emax - code, sign and mantissa kept.  Each block is the
+// packed dict's atom in AoS order, so the atom decoder of bf16x_device.h
+// serves both formats (decode_pairs<true>).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/bf16x_hip.h"
+#include "bf16x_device.h"
+#include "launch_common.h"
+
+namespace bf16x {
+namespace gguf {
+
+constexpr int kBlockBytes = 46;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)n, 0x00020000);
+}
+
+// 16-byte chunk q of block a of a pass: slot rotated by a/4 (conflict free for
+// per-block writes and contiguous reads)
+__device__ __forceinline__ int chunk_slot(int a, int q) { return a * 64 + (((q + (a >> 2)) & 3) << 4); }
+
+// ---------------------------------------------------------------------------
+// decode: one wave per row, 64 blocks per pass, staged through LDS so that
+// each store instruction writes contiguous bytes (1 KB bf16, 2 KB fp32)
+// ---------------------------------------------------------------------------
+template <bool F32>
+__global__ __launch_bounds__(256) void gguf_decode_kernel(const uint8_t* __restrict__ blocks, int64_t out_f,
+                                                          int64_t in_f, void* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 4096];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= out_f) return;
+  uint8_t* buf = lds + wave * 4096;
+  const int64_t P = in_f >> 5;
+  const int passes = (int)((P + 63) >> 6);
+  // descriptor based at the row (offsets < 4 GiB); it covers the rest of the
+  // blocks rounded up to 4 bytes, which the caller guarantees readable
+  const uint64_t row_off = (uint64_t)row * P * kBlockBytes;
+  const uint64_t total = ((uint64_t)out_f * P * kBlockBytes + 3) & ~3ull;
+  const __amdgpu_buffer_rsrc_t rs = rsrc(blocks + (row_off & ~3ull), total - (row_off & ~3ull));
+  const uint32_t skew = (uint32_t)(row_off & 3u);
+  auto load = [&](int c, GgufRaw& r) {
+    const uint32_t a = (uint32_t)min((int64_t)c * 64 + lane, P - 1);
+    load_gguf_raw(rs, skew + a * kBlockBytes, r);
+  };
+  GgufRaw cur, nxt;
+  load(0, cur);
+  for (int c = 0; c < passes; ++c) {
+    if (c + 1 < passes) load(c + 1, nxt);
+    uint32_t p[16];
+    decode_pairs<true>(gguf_atom(cur), p);
+    uint32_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      lo[i] = perm(p[2 * i + 1], p[2 * i], 0x05040100u);  // elements 2i, 2i+1
+      hi[i] = perm(p[2 * i + 1], p[2 * i], 0x07060302u);  // elements 16+2i, 17+2i
+    }
+    *(u32x4*)(buf + chunk_slot(lane, 0)) = u32x4{lo[0], lo[1], lo[2], lo[3]};
+    *(u32x4*)(buf + chunk_slot(lane, 1)) = u32x4{lo[4], lo[5], lo[6], lo[7]};
+    *(u32x4*)(buf + chunk_slot(lane, 2)) = u32x4{hi[0], hi[1], hi[2], hi[3]};
+    *(u32x4*)(buf + chunk_slot(lane, 3)) = u32x4{hi[4], hi[5], hi[6], hi[7]};
+    const int64_t col0 = (int64_t)c * 2048;
+    const int64_t nvalid = min((int64_t)2048, in_f - col0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = 8 * lane + 512 * i;
+      const u32x4 v = *(const u32x4*)(buf + chunk_slot(e >> 5, (e & 31) >> 3));
+      if (e < nvalid) {
+        if constexpr (F32) {
+          float* o = (float*)out + row * in_f + col0 + e;
+          const uint32_t v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
+          *(float4*)o = float4{bf16lo_to_f32(v0), bf16hi_to_f32(v0), bf16lo_to_f32(v1), bf16hi_to_f32(v1)};
+          *(float4*)(o + 4) = float4{bf16lo_to_f32(v2), bf16hi_to_f32(v2), bf16lo_to_f32(v3), bf16hi_to_f32(v3)};
+        } else {
+          *(u32x4a*)((uint16_t*)out + row * in_f + col0 + e) = v;
+        }
+      }
+    }
+    cur = nxt;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// x (bf16, in_f) -> pair order per 32-element atom: word i of atom a =
+// x[32a + i] | x[32a + 16 + i] << 16, the order decode_pairs produces
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void x_pairs_kernel(const uint16_t* __restrict__ x, int64_t in_f,
+                                                      uint32_t* __restrict__ xp) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;   // word index
+  if (i >= in_f / 2) return;
+  const int64_t a = i >> 4, j = i & 15;
+  xp[i] = (uint32_t)x[32 * a + j] | ((uint32_t)x[32 * a + 16 + j] << 16);
+}
+
+// ---------------------------------------------------------------------------
+// GEMV: one wave per row; lane l takes blocks l, l+64, ... of the row (loads
+// of consecutive lanes are contiguous) and the matching 64 bytes of paired x;
+// 16 v_dot2_f32_bf16 per block, wave sum by shuffles, y in bf16 or fp32.
+// Loads of the next pass are issued before the current one is used; lanes
+// past the row's end load its last block again and add nothing.
+// ---------------------------------------------------------------------------
+template <bool YF32>
+__global__ __launch_bounds__(256) void gguf_gemv_kernel(const uint8_t* __restrict__ blocks,
+                                                        const uint32_t* __restrict__ xp, int64_t out_f,
+                                                        int64_t in_f, void* __restrict__ y) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // XCD-aware row order: consecutive rows on one XCD
+  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
+  const int per = nb / 8, extra = nb - per * 8;
+  const int lb = nb >= 8 ? ((b & 7) * per + min(b & 7, extra) + (b >> 3)) : b;
+  const int64_t row = (int64_t)lb * 4 + wave;
+  if (row >= out_f) return;
+  const int64_t P = in_f >> 5;
+  const int passes = (int)((P + 63) >> 6);
+  const uint64_t row_off = (uint64_t)row * P * kBlockBytes;
+  const uint64_t total = ((uint64_t)out_f * P * kBlockBytes + 3) & ~3ull;
+  const __amdgpu_buffer_rsrc_t rs = rsrc(blocks + (row_off & ~3ull), total - (row_off & ~3ull));
+  const uint32_t skew = (uint32_t)(row_off & 3u);
+  const __amdgpu_buffer_rsrc_t rx = rsrc(xp, (uint64_t)in_f * 2);
+  struct Ld { GgufRaw t; u32x4 x[4]; };
+  auto load = [&](int c, Ld& l) {
+    const int64_t ai = (int64_t)c * 64 + lane;
+    const uint32_t a = (uint32_t)min(ai, P - 1);
+    load_gguf_raw(rs, skew + a * kBlockBytes, l.t);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) l.x[q] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(a * 64 + 16 * q), 0, 0);
+  };
+  float acc = 0.f;
+  Ld cur, nxt;
+  load(0, cur);
+  for (int c = 0; c < passes; ++c) {
+    if (c + 1 < passes) load(c + 1, nxt);
+    const bool live = (int64_t)c * 64 + lane < P;
+    uint32_t w[16];
+    decode_pairs<true>(gguf_atom(cur.t), w);
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const u32x4 xv = cur.x[q];
+      const uint32_t x0 = xv.x, x1 = xv.y, x2 = xv.z, x3 = xv.w;
+      s = dot2_bf16(w[4 * q + 0], x0, s);
+      s = dot2_bf16(w[4 * q + 1], x1, s);
+      s = dot2_bf16(w[4 * q + 2], x2, s);
+      s = dot2_bf16(w[4 * q + 3], x3, s);
+    }
+    acc += live ? s : 0.f;
+    cur = nxt;
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) {
+    if constexpr (YF32) ((float*)y)[row] = acc;
+    else ((uint16_t*)y)[row] = (uint16_t)f32_to_bf16_rne(acc);
+  }
+}
+
+}  // namespace gguf
+}  // namespace bf16x
+
+using namespace bf16x::gguf;
+
+namespace {
+
+int check_gguf(const void* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f) {
+  if (!blocks) return BF16X_EARG;
+  if (out_f <= 0 || in_f <= 0 || (in_f % 32) != 0) return BF16X_ESHAPE;
+  const int64_t nb = out_f * (in_f / 32);
+  if (nb > ((int64_t)1 << 31)) return BF16X_ESHAPE;
+  if (n_bytes < ((nb * kBlockBytes + 3) & ~(int64_t)3)) return BF16X_ESTREAM_LEN;
+  if ((in_f / 32) * kBlockBytes >= (int64_t)0xFFFFFFF0) return BF16X_ESHAPE;   // one row's offsets in 32 bits
+  return BF16X_OK;
+}
+
+}  // namespace
+
+extern "C" int bf16x_gguf_decode(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f, void* out,
+                                 int32_t out_dtype, bf16x_stream_t stream) {
+  int rc = check_gguf(blocks, n_bytes, out_f, in_f);
+  if (rc) return rc;
+  if (!out) return BF16X_EARG;
+  if (out_dtype != BF16X_BF16 && out_dtype != BF16X_F32) return BF16X_EDTYPE;
+  if (!aligned16(out) || !aligned4(blocks)) return BF16X_EARG;
+  const int64_t grid = (out_f + 3) / 4;
+  if (grid > INT32_MAX) return BF16X_ESHAPE;
+  hipStream_t st = (hipStream_t)stream;
+  if (out_dtype == BF16X_F32)
+    hipLaunchKernelGGL(gguf_decode_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, blocks, out_f, in_f, out);
+  else
+    hipLaunchKernelGGL(gguf_decode_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, blocks, out_f, in_f, out);
+  return launch_status();
+}
+
+extern "C" int64_t bf16x_gguf_gemv_workspace(int64_t in_f) { return in_f > 0 ? in_f * 2 : 0; }
+
+extern "C" int bf16x_gguf_gemv(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes, int64_t out_f,
+                               int64_t in_f, void* y, int32_t y_dtype, void* workspace, int64_t workspace_bytes,
+                               bf16x_stream_t stream) {
+  int rc = check_gguf(blocks, n_bytes, out_f, in_f);
+  if (rc) return rc;
+  if (!x || !y || !workspace) return BF16X_EARG;
+  if (x_dtype != BF16X_BF16 || (y_dtype != BF16X_BF16 && y_dtype != BF16X_F32)) return BF16X_EDTYPE;
+  if (workspace_bytes < in_f * 2) return BF16X_ECAPACITY;
+  if (!aligned2(x) || !aligned16(workspace) || !aligned4(blocks) || !aligned4(y)) return BF16X_EARG;
+  const int64_t grid = (out_f + 3) / 4;
+  if (grid > INT32_MAX) return BF16X_ESHAPE;
+  hipStream_t st = (hipStream_t)stream;
+  uint32_t* xp = (uint32_t*)workspace;
+  hipLaunchKernelGGL(x_pairs_kernel, dim3((unsigned)((in_f / 2 + 255) / 256)), dim3(256), 0, st, (const uint16_t*)x,
+                     in_f, xp);
+  if (y_dtype == BF16X_F32)
+    hipLaunchKernelGGL(gguf_gemv_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, blocks, xp, out_f, in_f, y);
+  else
+    hipLaunchKernelGGL(gguf_gemv_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, blocks, xp, out_f, in_f, y);
+  return launch_status();
+}

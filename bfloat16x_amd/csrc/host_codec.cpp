@@ -221,3 +221,56 @@ extern "C" int bf16x_plan_host(const int32_t* ovf_idx, const uint8_t* ovf_val, i
   }
   return BF16X_OK;
 }
+
+// ---------------------------------------------------------------------------
+// GGUF half-block codec (bf16x_gguf_block.py:29-73)
+// ---------------------------------------------------------------------------
+
+// fp32 -> bf16 bits as fp32_to_bf16_bits (bf16x_gguf_block.py:44-49): NaNs
+// get the quiet bit (bit 22) before the round-to-nearest-even add, whose
+// carry may run into the sign for the largest NaN patterns, as there.
+extern "C" int bf16x_fp32_to_bf16_host(const float* x, int64_t n, uint16_t* out, int32_t n_threads) {
+  if (n < 0 || (n > 0 && (!x || !out))) return BF16X_EARG;
+  parallel_for(n, host_threads(n_threads), [&](int64_t b, int64_t e) {
+    for (int64_t i = b; i < e; ++i) {
+      uint32_t u;
+      memcpy(&u, x + i, 4);
+      if ((u & 0x7FFFFFFFu) > 0x7F800000u) u = (u & 0xFFFF0000u) | 0x00400000u;
+      out[i] = (uint16_t)(((uint64_t)u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+    }
+  });
+  return BF16X_OK;
+}
+
+// bf16 bits (n_blocks * 32, row-major) -> n_blocks 46-byte blocks
+// (bf16x_gguf_block.py:57-73): emax per 16-element half floored at 7,
+// code = min(emax - e, 7), fields LSB-first.
+extern "C" int bf16x_gguf_quantize_host(const uint16_t* bits, int64_t n_blocks, uint8_t* out, int32_t n_threads) {
+  if (n_blocks < 0 || (n_blocks > 0 && (!bits || !out))) return BF16X_EARG;
+  parallel_for(n_blocks, host_threads(n_threads), [&](int64_t b, int64_t e) {
+    for (int64_t k = b; k < e; ++k) {
+      const uint16_t* w = bits + 32 * k;
+      uint8_t* o = out + 46 * k;
+      uint32_t emax[2] = {7u, 7u};
+      for (int j = 0; j < 32; ++j) emax[j >> 4] = std::max(emax[j >> 4], (uint32_t)((w[j] >> 7) & 0xFF));
+      uint32_t sign = 0, mw[7] = {0, 0, 0, 0, 0, 0, 0}, dw[3] = {0, 0, 0};
+      for (int j = 0; j < 32; ++j) {
+        const uint32_t ex = (w[j] >> 7) & 0xFF;
+        sign |= (uint32_t)(w[j] >> 15) << j;
+        const uint64_t mb = 7 * j, db = 3 * j;
+        const uint64_t m = (uint64_t)(w[j] & 0x7F) << (mb & 31);
+        mw[mb >> 5] |= (uint32_t)m;
+        if ((mb & 31) + 7 > 32) mw[(mb >> 5) + 1] |= (uint32_t)(m >> 32);
+        const uint64_t d = (uint64_t)std::min<uint32_t>(emax[j >> 4] - ex, 7u) << (db & 31);
+        dw[db >> 5] |= (uint32_t)d;
+        if ((db & 31) + 3 > 32) dw[(db >> 5) + 1] |= (uint32_t)(d >> 32);
+      }
+      o[0] = (uint8_t)emax[0];
+      o[1] = (uint8_t)emax[1];
+      memcpy(o + 2, &sign, 4);
+      memcpy(o + 6, mw, 28);
+      memcpy(o + 34, dw, 12);
+    }
+  });
+  return BF16X_OK;
+}

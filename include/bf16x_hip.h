@@ -178,6 +178,40 @@ int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M,
                void* y, int32_t y_dtype, void* workspace, int64_t workspace_bytes,
                bf16x_stream_t stream);
 
+/* ========================================================================
+ * GGUF half-block variant (bf16x_gguf_block.py, GGML_TYPE_BF16X): blocks of
+ * 32 row-major weights, 46 bytes = [emax[2] | sign[4] | mant[28] |
+ * delta[12]], emax floored at 7, code min(emax - e, 7), code 7 decodes to
+ * exponent 0 (zero marker, :84).  A weight [out_f, in_f] (in_f % 32 == 0)
+ * is out_f * in_f / 32 consecutive blocks.  Device block buffers must be
+ * 4-byte aligned and readable up to the block bytes rounded up to a
+ * multiple of 4 (n_bytes counts that length).
+ * ======================================================================== */
+
+/* fp32 -> bf16 bits with the reference's rounding (fp32_to_bf16_bits,
+ * bf16x_gguf_block.py:44-49: NaN quieted, then round to nearest even).
+ * Host pointers; n_threads <= 0 = hardware concurrency. */
+int bf16x_fp32_to_bf16_host(const float* x, int64_t n, uint16_t* out, int32_t n_threads);
+
+/* bf16 bits [n_blocks * 32] -> blocks [n_blocks * 46] (quantize_blocks,
+ * bf16x_gguf_block.py:57-73, after its fp32 -> bf16 rounding).  Host. */
+int bf16x_gguf_quantize_host(const uint16_t* bits, int64_t n_blocks, uint8_t* out, int32_t n_threads);
+
+/* Device decode (dequantize_blocks, bf16x_gguf_block.py:76-87): blocks ->
+ * out [out_f, in_f] of out_dtype BF16X_BF16 or BF16X_F32 (16-byte aligned). */
+int bf16x_gguf_decode(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f,
+                      void* out, int32_t out_dtype, bf16x_stream_t stream);
+
+/* Device decode + GEMV, y[out_f] = W . x, x bf16 [in_f], y of y_dtype
+ * (BF16X_BF16 / BF16X_F32), fp32 accumulation.  The reference keeps this
+ * product in llama.cpp's GGML_TYPE_BF16X mat-vec kernels (README.md:121,
+ * 138), outside the Python sources.  workspace: dev, 16-byte aligned,
+ * bf16x_gguf_gemv_workspace(in_f) bytes (x rearranged in decode order). */
+int64_t bf16x_gguf_gemv_workspace(int64_t in_f);
+int bf16x_gguf_gemv(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes,
+                    int64_t out_f, int64_t in_f, void* y, int32_t y_dtype,
+                    void* workspace, int64_t workspace_bytes, bf16x_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
