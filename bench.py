@@ -16,7 +16,10 @@ Secondary fields (same rotation): the exact decode kernel's time and
 read+write bandwidth, and decode+GEMM (configuration 3) at --gemm-rows
 activation rows through the fused kernel ("fused") and the default dispatch
 ("auto": fused below 256 rows, decode + hipBLASLt from 256 rows on), with
-torch bf16 F.linear on the decoded weight beside them.
+torch bf16 F.linear on the decoded weight beside them; and configuration 5
+(GGUF half-block, 8192x28672 and 28672x8192, Student-t(3) x 0.015): fused
+decode+GEMV, decode, decode+GEMM at M = 512, clamped fraction and max abs
+reconstruction error.
 Printed as one JSON line; diagnostics go to stderr.
 """
 from __future__ import annotations
@@ -99,6 +102,52 @@ def cpu_baseline(d: dict, alg_bytes_full: int, rows: int) -> dict:
             "seconds_per_sample": round(ts[1], 4), "cpu": cpu}
 
 
+def bench_gguf(bx, dev, stream) -> list:
+    """GGUF decode+GEMV (batch 1) and decode+GEMM (M = 512) at 8192x28672 and
+    28672x8192, two rotating copies (> 2x the Infinity Cache); max abs
+    reconstruction error of the decode against bf16(w)."""
+    import numpy as np
+    out = []
+    for out_f, in_f in ((8192, 28672), (28672, 8192)):
+        t = time.time()
+        rng = np.random.default_rng(0)
+        w = (rng.standard_t(3, size=(out_f, in_f)) * 0.015).astype(np.float32)
+        blocks = bx.gguf.quantize_blocks(w)
+        wb = torch.from_numpy(bx.gguf.fp32_to_bf16_bits(w).view(np.int16)).to(dev).view(torch.bfloat16)
+        del w
+        copies = [bx.gguf.device_blocks(blocks, dev) for _ in range(2)]
+        nbytes = blocks.size
+        del blocks
+        log(f"gguf {out_f}x{in_f}: weights + encode {time.time() - t:.1f}s")
+        dec = bx.gguf.gguf_decode(copies[0], out_f, in_f)
+        err = (dec.float() - wb.float()).abs().max().item()
+        clamped = (dec.view(torch.int16) != wb.view(torch.int16)).float().mean().item()
+        del dec
+        x = torch.randn(in_f, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+        sec_v = time_launches(lambda i: bx.gguf.gguf_gemv(x, copies[i % 2], out_f, in_f), 200, 20, stream)
+        dec_out = torch.empty(out_f, in_f, dtype=torch.bfloat16, device=dev)
+        sec_d = time_launches(lambda i: bx.gguf.gguf_decode(copies[i % 2], out_f, in_f, out=dec_out), 30, 4, stream)
+        del dec_out
+        xm = torch.randn(512, in_f, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
+        sec_m = time_launches(lambda i: bx.gguf.gguf_gemm(xm, copies[i % 2], out_f, in_f), 10, 2, stream)
+        wcopies = [wb, wb.clone()]
+        sec_bv = time_launches(lambda i: torch.nn.functional.linear(x.view(1, -1), wcopies[i % 2]), 100, 10, stream)
+        del wcopies, wb, copies, xm
+        torch.cuda.empty_cache()
+        vbytes = nbytes + 2 * in_f + 2 * out_f
+        ent = {"shape": [out_f, in_f], "block_bytes": nbytes,
+               "gemv_us": round(sec_v * 1e6, 2), "gemv_GBps": round(vbytes / sec_v / 1e9, 1),
+               "gemv_hbm_frac": round(vbytes / sec_v / 1e9 / HBM_PEAK_GBS, 4),
+               "bf16_gemv_us": round(sec_bv * 1e6, 2), "speedup_vs_bf16_gemv": round(sec_bv / sec_v, 3),
+               "decode_us": round(sec_d * 1e6, 2),
+               "gemm_M512_us": round(sec_m * 1e6, 2),
+               "gemm_M512_tflops": round(2.0 * 512 * out_f * in_f / sec_m / 1e12, 1),
+               "clamped_fraction": round(clamped, 5), "max_abs_reconstruction_error": err}
+        log(f"gguf {ent}")
+        out.append(ent)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -106,6 +155,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=7168)
+    ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF (configuration 5) lines")
     ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 2048],
                     help="activation rows of the decode+GEMM lines (configuration 3)")
     args = ap.parse_args()
@@ -210,6 +260,13 @@ def main():
         log(f"gemm {ent}")
         del xm
 
+    # ---- configuration 5: GGUF half-block, 70B-layer shapes, Student-t(3) x 0.015
+    gguf_rec = None
+    if not args.no_gguf:
+        del copies, argv
+        torch.cuda.empty_cache()
+        gguf_rec = bench_gguf(bx, dev, stream)
+
     cpu = None
     if not args.no_cpu:
         t = time.time()
@@ -240,6 +297,7 @@ def main():
         "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 2),
         "decode_exact_14336x4096": decode_rec,
         "gemm_14336x4096_exact": gemm_rec,
+        "gguf_config5": gguf_rec,
     }
     print(json.dumps(rec), flush=True)
 
