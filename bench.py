@@ -102,6 +102,18 @@ def cpu_baseline(d: dict, alg_bytes_full: int, rows: int) -> dict:
             "seconds_per_sample": round(ts[1], 4), "cpu": cpu}
 
 
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed counter profile of this
+    workload (profiles/gemv_14336x4096_exact_traffic.json: FETCH_SIZE and
+    WRITE_SIZE per dispatch scaled by a copy kernel of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "gemv_14336x4096_exact_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["hbm_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def bench_gguf(bx, dev, stream) -> list:
     """GGUF decode+GEMV (batch 1) and decode+GEMM (M = 512) at 8192x28672 and
     28672x8192, two rotating copies (> 2x the Infinity Cache); max abs
@@ -156,6 +168,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=7168)
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF (configuration 5) lines")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 2048],
                     help="activation rows of the decode+GEMM lines (configuration 3)")
     args = ap.parse_args()
@@ -211,6 +225,17 @@ def main():
     sec = time_launches(step, args.steps, args.warmup, stream)
     gbs = abytes / sec / 1e9
     log(f"bf16x gemv: {sec * 1e6:.2f} us/launch, {gbs:.1f} GB/s algorithmic ({n_copies} rotating copies)")
+
+    if args.calib_copy:
+        # a plain device copy of known size (1 GiB read, 1 GiB written) for
+        # scaling the FETCH_SIZE / WRITE_SIZE counters of a --pmc run
+        src = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        log("calibration copy: 3 x 1 GiB")
 
     # plain bf16 GEMV comparator (torch / hipBLASLt) with the same rotation
     wcopies = [wd] + [wd.clone() for _ in range(max(1, -(-3 * MALL_BYTES // (wd.numel() * 2))) - 1)]
@@ -290,7 +315,7 @@ def main():
                    "out_f": out_f, "in_f": in_f, "weights": "N(0,0.02), 1% x30, seed 0",
                    "rotating_copies": n_copies, "alg_bytes_per_launch": abytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
         "bf16_gemv_us": round(sec_bf16 * 1e6, 3),
         "speedup_vs_bf16_gemv": round(sec_bf16 / sec, 3),
