@@ -7,16 +7,21 @@ Call surface (mirrors the reference dfytensor/bfloat16x):
   bf16x_fused_gemm                     bf16x_gemm_fused.py:97
   gguf.quantize_blocks / dequantize_blocks / quantize_tensor / fp32_to_bf16_bits
                                        bf16x_gguf_block.py:44-93
+  Bf16xFused, deploy_bf16x_fused       bf16x_fused.py:149-263
+  Bf16xGemmLinear, deploy_bf16x_gemm   bf16x_gemm_fused.py:154-242
+  BF16XLinear                          opqk_linear.py:327-407
 All GPU work runs in the HIP library libbf16x_hip.so through its C ABI
 (include/bf16x_hip.h).
 """
 from ._lib import Bf16xError, version
 from .codec import Bf16xPlan, bf16x_quantize, build_plan_host, stream_words
 from . import gguf
+from .nn import BF16XLinear, Bf16xFused, Bf16xGemmLinear, deploy_bf16x_fused, deploy_bf16x_gemm
 from .ops import (bf16x_decode, bf16x_decode_triton, bf16x_fused_gemm, bf16x_fused_gemv, bf16x_gemm,
                   bf16x_gemv)
 
 __all__ = [
+    "BF16XLinear", "Bf16xFused", "Bf16xGemmLinear", "deploy_bf16x_fused", "deploy_bf16x_gemm",
     "Bf16xError", "Bf16xPlan", "bf16x_decode", "bf16x_decode_triton", "bf16x_fused_gemm", "bf16x_fused_gemv",
     "bf16x_gemm", "bf16x_gemv",
     "bf16x_quantize", "build_plan_host", "gguf", "stream_words", "version",
