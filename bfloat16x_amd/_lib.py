@@ -1,4 +1,5 @@
-"""ctypes binding of libbf16x_hip.so (the C ABI declared in include/bf16x_hip.h).
+"""ctypes binding of libbf16x_hip.so (the C ABI declared in include/bf16x_hip.h and
+include/bf16x_llama.h).
 
 torch is imported first on purpose: torch ships its own HIP runtime
 (torch/lib/libamdhip64.so, soname libamdhip64.so.7).  Loading this library
@@ -23,7 +24,7 @@ EXACT, SATURATED = 0, 1
 _c_i32, _c_i64, _c_u32 = ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32
 _P = ctypes.c_void_p
 
-# name -> (restype, argtypes); every function of include/bf16x_hip.h
+# name -> (restype, argtypes); every function of include/bf16x_hip.h and include/bf16x_llama.h
 PROTOTYPES = {
     "bf16x_version": (ctypes.c_char_p, []),
     "bf16x_status_string": (ctypes.c_char_p, [ctypes.c_int]),
@@ -48,6 +49,13 @@ PROTOTYPES = {
     "bf16x_gguf_decode": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i64, _P, _c_i32, _P]),
     "bf16x_gguf_gemv_workspace": (_c_i64, [_c_i64]),
     "bf16x_gguf_gemv": (ctypes.c_int, [_P, _c_i32, _P, _c_i64, _c_i64, _c_i64, _P, _c_i32, _P, _c_i64, _P]),
+    # include/bf16x_llama.h
+    "bf16x_rmsnorm": (ctypes.c_int, [_P, _P, _c_i64, _P, _P, _P, _c_i64, _c_i64, ctypes.c_float, _c_i32, _P]),
+    "bf16x_rope_kv": (ctypes.c_int, [_P, _c_i64, _P, _P, _c_i64, _c_i64, _c_i64, _c_i64, _P, _P, _P, _P]),
+    "bf16x_attention": (ctypes.c_int, [_P, _P, _P, _P, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float,
+                                       _P, _P]),
+    "bf16x_silu_mul": (ctypes.c_int, [_P, _c_i64, _c_i64, _P, _P]),
+    "bf16x_greedy": (ctypes.c_int, [_P, _c_i64, _P, _P, _P, _c_i64, _P]),
 }
 
 _LIB = None

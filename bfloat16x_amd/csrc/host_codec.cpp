@@ -10,7 +10,10 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <sched.h>
+
 #include <algorithm>
+#include <cstdlib>
 #include <thread>
 #include <vector>
 
@@ -26,10 +29,18 @@ int64_t words_of(int64_t n, int32_t b) {
   return (nbits + 31) / 32;
 }
 
+// Default thread count: the CPUs this process may run on (affinity mask),
+// capped by OMP_NUM_THREADS when set (the share a job scheduler grants) and 64.
 int host_threads(int32_t req) {
   if (req > 0) return req;
-  unsigned hc = std::thread::hardware_concurrency();
-  return hc ? (int)std::min<unsigned>(hc, 64) : 4;
+  int n = (int)std::thread::hardware_concurrency();
+  cpu_set_t set;
+  if (sched_getaffinity(0, sizeof(set), &set) == 0 && CPU_COUNT(&set) > 0) n = CPU_COUNT(&set);
+  if (const char* e = std::getenv("OMP_NUM_THREADS")) {
+    const int v = std::atoi(e);
+    if (v > 0) n = std::min(n, v);
+  }
+  return n > 0 ? std::min(n, 64) : 4;
 }
 
 template <class F>

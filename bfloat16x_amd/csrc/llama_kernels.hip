@@ -1,0 +1,370 @@
+// Decoder-stack kernels of the Llama-style harness (include/bf16x_llama.h):
+// everything of one decoder layer except the BF16X linears, as few launches
+// as the data dependences allow, so that a decode step is a fixed launch
+// sequence a HIP graph captures.  The token position is read from device
+// memory (`pos`, `state`), never passed by value, so one captured graph
+// serves every step.
+//
+// All of these are small next to the linears at batch 1 (a few MB per layer
+// against ~340 MB of packed weights): they are written for few launches and
+// plain coalesced access, not for peak bandwidth.
+#include "bf16x_device.h"
+#include "launch_common.h"
+#include "../../include/bf16x_llama.h"
+
+namespace {
+using namespace bf16x;
+
+__device__ __forceinline__ float bfv(uint32_t b16) { return __uint_as_float(b16 << 16); }
+__device__ __forceinline__ uint16_t to_bf(float f) { return (uint16_t)f32_to_bf16_rne(f); }
+__device__ __forceinline__ float round_bf(float f) { return bfv(f32_to_bf16_rne(f)); }
+
+// Sum over a 256-thread block; every thread gets the total.  `red` holds 4
+// floats; the trailing barrier lets the caller reuse it.
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  const float t = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return t;
+}
+
+__device__ __forceinline__ float block_max256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  const float t = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  return t;
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm with the residual stream: one block of 256 threads per row, a
+// thread holds up to 4 chunks of 8 elements (n <= 8192) in registers between
+// the sum of squares and the scaling.
+constexpr int kNormChunks = 4;
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict__ x,
+                                                      const int64_t* __restrict__ row_idx, int64_t x_rows,
+                                                      uint16_t* __restrict__ res, const uint16_t* __restrict__ w,
+                                                      uint16_t* __restrict__ out, int n, float eps, int flags) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  int64_t xr = r;
+  if (row_idx) {
+    const int64_t t = row_idx[r];
+    xr = t < 0 ? 0 : (t >= x_rows ? x_rows - 1 : t);
+  }
+  const uint16_t* xp = x + xr * n;
+  uint16_t* rp = res ? res + r * n : nullptr;
+  float h[kNormChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int i = (c * 256 + (int)threadIdx.x) * 8;
+    if (i < n) {
+      const u32x4 xv = *(const u32x4*)(xp + i);
+      u32x4 rv = {0u, 0u, 0u, 0u};
+      if (flags & BF16X_NORM_ADD) rv = *(const u32x4*)(rp + i);
+      const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w};
+      const uint32_t rw[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float a = bf16lo_to_f32(xw[k]), b = bf16hi_to_f32(xw[k]);
+        if (flags & BF16X_NORM_ADD) {
+          a = round_bf(a + bf16lo_to_f32(rw[k]));
+          b = round_bf(b + bf16hi_to_f32(rw[k]));
+        }
+        h[c][2 * k] = a;
+        h[c][2 * k + 1] = b;
+        ss += a * a + b * b;
+      }
+      if (flags & BF16X_NORM_STORE) {
+        u32x4 hv;
+        hv.x = f32_to_bf16_rne(h[c][0]) | (f32_to_bf16_rne(h[c][1]) << 16);
+        hv.y = f32_to_bf16_rne(h[c][2]) | (f32_to_bf16_rne(h[c][3]) << 16);
+        hv.z = f32_to_bf16_rne(h[c][4]) | (f32_to_bf16_rne(h[c][5]) << 16);
+        hv.w = f32_to_bf16_rne(h[c][6]) | (f32_to_bf16_rne(h[c][7]) << 16);
+        *(u32x4*)(rp + i) = hv;
+      }
+    }
+  }
+  const float tot = block_sum256(ss, red);
+  const float s = 1.0f / sqrtf(tot / (float)n + eps);
+  uint16_t* op = out + r * n;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int i = (c * 256 + (int)threadIdx.x) * 8;
+    if (i < n) {
+      const u32x4 wv = *(const u32x4*)(w + i);
+      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float a = round_bf(h[c][2 * k] * s) * bf16lo_to_f32(ww[k]);
+        const float b = round_bf(h[c][2 * k + 1] * s) * bf16hi_to_f32(ww[k]);
+        o[k] = f32_to_bf16_rne(a) | (f32_to_bf16_rne(b) << 16);
+      }
+      *(u32x4*)(op + i) = u32x4{o[0], o[1], o[2], o[3]};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rotary embedding + KV append.  One wave per (token, head) of the fused qkv
+// row; lane i owns dims i and i + 64 (the rotate-half pair).  head_dim 128.
+__global__ __launch_bounds__(256) void rope_kv_kernel(const uint16_t* __restrict__ qkv, const int32_t* __restrict__ pos,
+                                                      const float* __restrict__ cs, int H, int KV, int max_len,
+                                                      uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+                                                      uint16_t* __restrict__ vc) {
+  const int t = blockIdx.x;
+  const int hw = blockIdx.y * 4 + (int)(threadIdx.x >> 6);
+  const int i = threadIdx.x & 63;
+  if (hw >= H + 2 * KV) return;
+  const int p = pos[0] + t;
+  const uint16_t* src = qkv + ((int64_t)t * (H + 2 * KV) + hw) * 128;
+  const uint16_t a16 = src[i], b16 = src[i + 64];
+  if (hw >= H + KV) {                       // v head: plain copy into the cache
+    if (p >= 0 && p < max_len) {
+      uint16_t* dst = vc + ((int64_t)(hw - H - KV) * max_len + p) * 128;
+      dst[i] = a16;
+      dst[i + 64] = b16;
+    }
+    return;
+  }
+  const int pc = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
+  const float c = cs[((int64_t)pc * 64 + i) * 2], s = cs[((int64_t)pc * 64 + i) * 2 + 1];
+  const float a = bfv(a16), b = bfv(b16);
+  const uint16_t ra = to_bf(a * c - b * s), rb = to_bf(b * c + a * s);
+  if (hw < H) {
+    uint16_t* dst = q_out + ((int64_t)t * H + hw) * 128;
+    dst[i] = ra;
+    dst[i + 64] = rb;
+  } else if (p >= 0 && p < max_len) {
+    uint16_t* dst = kc + ((int64_t)(hw - H) * max_len + p) * 128;
+    dst[i] = ra;
+    dst[i + 64] = rb;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Causal GQA attention, one block per (head, query).  Scores: a thread per
+// key (the 256-byte key row read as 16 dwordx4, q broadcast from LDS);
+// softmax over the scores kept in LDS; P.V: wave w takes keys j = w mod 4,
+// lane l dims 2l, 2l+1 (one coalesced 256-byte row per key), the four
+// partial sums reduced through LDS.  head_dim 128.
+__global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restrict__ q,
+                                                        const uint16_t* __restrict__ kc,
+                                                        const uint16_t* __restrict__ vc,
+                                                        const int32_t* __restrict__ pos, int H, int KV, int max_len,
+                                                        float scale, uint16_t* __restrict__ out) {
+  extern __shared__ float sc[];           // [max_len] scores, then probabilities
+  __shared__ float qs[128];
+  __shared__ float red[4];
+  __shared__ float part[4][128];
+  const int h = blockIdx.x, t = blockIdx.y;
+  const int kvh = h / (H / KV);
+  const int p = pos[0] + t;
+  const int n = p + 1 < 0 ? 0 : (p + 1 > max_len ? max_len : p + 1);
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  uint16_t* op = out + ((int64_t)t * H + h) * 128;
+  if (tid < 128) qs[tid] = bfv(q[((int64_t)t * H + h) * 128 + tid]) * scale;
+  __syncthreads();
+  const uint16_t* K = kc + (int64_t)kvh * max_len * 128;
+  float mx = -INFINITY;
+  for (int j = tid; j < n; j += 256) {
+    const u32x4* kr = (const u32x4*)(K + (int64_t)j * 128);
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int c = 0; c < 16; ++c) {
+      const u32x4 kv = kr[c];
+      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        s0 = fmaf(qs[8 * c + 2 * e], bf16lo_to_f32(kw[e]), s0);
+        s1 = fmaf(qs[8 * c + 2 * e + 1], bf16hi_to_f32(kw[e]), s1);
+      }
+    }
+    const float s = s0 + s1;
+    sc[j] = s;
+    mx = fmaxf(mx, s);
+  }
+  const float M = block_max256(mx, red);
+  float sum = 0.f;
+  for (int j = tid; j < n; j += 256) {
+    const float e = __expf(sc[j] - M);
+    sc[j] = e;
+    sum += e;
+  }
+  const float L = block_sum256(sum, red);   // its barriers also publish sc[]
+  const uint32_t* V = (const uint32_t*)(vc + (int64_t)kvh * max_len * 128);
+  float a0 = 0.f, a1 = 0.f, b0 = 0.f, b1 = 0.f;
+  int j = wv;
+  for (; j + 4 < n; j += 8) {
+    const uint32_t v0 = V[(int64_t)j * 64 + lane], v1 = V[(int64_t)(j + 4) * 64 + lane];
+    const float p0 = sc[j], p1 = sc[j + 4];
+    a0 = fmaf(p0, bf16lo_to_f32(v0), a0);
+    a1 = fmaf(p0, bf16hi_to_f32(v0), a1);
+    b0 = fmaf(p1, bf16lo_to_f32(v1), b0);
+    b1 = fmaf(p1, bf16hi_to_f32(v1), b1);
+  }
+  if (j < n) {
+    const uint32_t v0 = V[(int64_t)j * 64 + lane];
+    a0 = fmaf(sc[j], bf16lo_to_f32(v0), a0);
+    a1 = fmaf(sc[j], bf16hi_to_f32(v0), a1);
+  }
+  part[wv][2 * lane] = a0 + b0;
+  part[wv][2 * lane + 1] = a1 + b1;
+  __syncthreads();
+  if (tid < 128) {
+    const float o = (part[0][tid] + part[1][tid]) + (part[2][tid] + part[3][tid]);
+    op[tid] = n > 0 ? to_bf(o / L) : (uint16_t)0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU over 8 columns per thread.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t T, int F,
+                                                       uint16_t* __restrict__ out) {
+  const int64_t chunks = T * (F / 8);
+  for (int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x; id < chunks; id += (int64_t)gridDim.x * 256) {
+    const int64_t t = id / (F / 8);
+    const int c = (int)(id - t * (F / 8)) * 8;
+    const u32x4 gv = *(const u32x4*)(gu + t * 2 * F + c);
+    const u32x4 uv = *(const u32x4*)(gu + t * 2 * F + F + c);
+    const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w}, u[4] = {uv.x, uv.y, uv.z, uv.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float g0 = bf16lo_to_f32(g[k]), g1 = bf16hi_to_f32(g[k]);
+      const float s0 = round_bf(g0 / (1.0f + __expf(-g0))), s1 = round_bf(g1 / (1.0f + __expf(-g1)));
+      o[k] = f32_to_bf16_rne(s0 * bf16lo_to_f32(u[k])) | (f32_to_bf16_rne(s1 * bf16hi_to_f32(u[k])) << 16);
+    }
+    *(u32x4*)(out + t * F + c) = u32x4{o[0], o[1], o[2], o[3]};
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Greedy step: one block of 1024 threads, (value, index) reduced with the
+// first index winning ties, then the token, history and counters written by
+// thread 0.
+__device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
+  if (v2 > v || (v2 == v && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+__global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t* __restrict__ logits, int V,
+                                                      int64_t* __restrict__ token, int32_t* __restrict__ state,
+                                                      int32_t* __restrict__ hist, int hist_len) {
+  __shared__ float rv[16];
+  __shared__ int ri[16];
+  float bv = -INFINITY;
+  int bi = 0x7FFFFFFF;
+  const int tid = threadIdx.x;
+  const int full = V & ~7;
+  for (int i = tid * 8; i < full; i += 1024 * 8) {
+    const u32x4 v = *(const u32x4*)(logits + i);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      better(bv, bi, bf16lo_to_f32(w[k]), i + 2 * k);
+      better(bv, bi, bf16hi_to_f32(w[k]), i + 2 * k + 1);
+    }
+  }
+  if (tid < V - full) better(bv, bi, bfv(logits[full + tid]), full + tid);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+  if ((tid & 63) == 0) {
+    rv[tid >> 6] = bv;
+    ri[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int k = 1; k < 16; ++k) better(bv, bi, rv[k], ri[k]);
+    if (bi == 0x7FFFFFFF) bi = 0;        // every logit NaN: token 0
+    token[0] = bi;
+    const int c = state[1];
+    if (c >= 0 && c < hist_len) hist[c] = bi;
+    state[1] = c + 1;
+    state[0] = state[0] + 1;
+  }
+}
+
+}  // namespace
+
+extern "C" int bf16x_rmsnorm(const uint16_t* x, const int64_t* row_idx, int64_t x_rows, uint16_t* residual,
+                             const uint16_t* weight, uint16_t* out, int64_t rows, int64_t n, float eps, int32_t flags,
+                             bf16x_stream_t stream) {
+  if (!x || !weight || !out || rows < 0 || (flags & ~(BF16X_NORM_ADD | BF16X_NORM_STORE))) return BF16X_EARG;
+  if (n <= 0 || n % 8 != 0 || n > kNormChunks * 256 * 8 || rows > INT32_MAX) return BF16X_ESHAPE;
+  if (row_idx && x_rows <= 0) return BF16X_EARG;
+  if (flags && !residual) return BF16X_EARG;
+  if (!aligned16(x) || !aligned16(weight) || !aligned16(out) || (residual && !aligned16(residual)))
+    return BF16X_EARG;
+  if (rows == 0) return BF16X_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream, x, row_idx, x_rows,
+                     residual, weight, out, (int)n, eps, (int)flags);
+  return launch_status();
+}
+
+extern "C" int bf16x_rope_kv(const uint16_t* qkv, int64_t tokens, const int32_t* pos, const float* cos_sin,
+                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t max_len, uint16_t* q_out,
+                             uint16_t* k_cache, uint16_t* v_cache, bf16x_stream_t stream) {
+  if (!qkv || !pos || !cos_sin || !q_out || !k_cache || !v_cache || tokens < 0) return BF16X_EARG;
+  if (head_dim != 128 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads > 4096 ||
+      max_len <= 0 || max_len > INT32_MAX / 2 || tokens > 65535)
+    return BF16X_ESHAPE;
+  if (!aligned4(cos_sin) || !aligned2(qkv) || !aligned2(q_out) || !aligned2(k_cache) || !aligned2(v_cache))
+    return BF16X_EARG;
+  if (tokens == 0) return BF16X_OK;
+  const int heads = (int)(n_heads + 2 * n_kv_heads);
+  hipLaunchKernelGGL(rope_kv_kernel, dim3((unsigned)tokens, (unsigned)((heads + 3) / 4)), dim3(256), 0,
+                     (hipStream_t)stream, qkv, pos, cos_sin, (int)n_heads, (int)n_kv_heads, (int)max_len, q_out,
+                     k_cache, v_cache);
+  return launch_status();
+}
+
+extern "C" int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                               const int32_t* pos, int64_t tokens, int64_t n_heads, int64_t n_kv_heads,
+                               int64_t head_dim, int64_t max_len, float scale, uint16_t* out,
+                               bf16x_stream_t stream) {
+  if (!q || !k_cache || !v_cache || !pos || !out || tokens < 0) return BF16X_EARG;
+  if (head_dim != 128 || n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads > 65535 ||
+      max_len <= 0 || max_len > 16384 || tokens > 65535)
+    return BF16X_ESHAPE;
+  if (!aligned16(k_cache) || !aligned4(v_cache) || !aligned2(q) || !aligned2(out)) return BF16X_EARG;
+  if (tokens == 0) return BF16X_OK;
+  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)n_heads, (unsigned)tokens), dim3(256),
+                     (size_t)max_len * sizeof(float), (hipStream_t)stream, q, k_cache, v_cache, pos, (int)n_heads,
+                     (int)n_kv_heads, (int)max_len, scale, out);
+  return launch_status();
+}
+
+extern "C" int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t ffn, uint16_t* out,
+                              bf16x_stream_t stream) {
+  if (!gate_up || !out || tokens < 0) return BF16X_EARG;
+  if (ffn <= 0 || ffn % 8 != 0 || ffn > INT32_MAX / 2) return BF16X_ESHAPE;
+  if (!aligned16(gate_up) || !aligned16(out)) return BF16X_EARG;
+  if (tokens == 0) return BF16X_OK;
+  const int64_t chunks = tokens * (ffn / 8);
+  const int64_t grid = std::min<int64_t>((chunks + 255) / 256, 8192);
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, gate_up, tokens,
+                     (int)ffn, out);
+  return launch_status();
+}
+
+extern "C" int bf16x_greedy(const uint16_t* logits, int64_t vocab, int64_t* token, int32_t* state, int32_t* history,
+                            int64_t history_len, bf16x_stream_t stream) {
+  if (!logits || !token || !state || (!history && history_len > 0) || history_len < 0) return BF16X_EARG;
+  if (vocab <= 0 || vocab > INT32_MAX - 8 * 1024 || history_len > INT32_MAX) return BF16X_ESHAPE;
+  if (!aligned16(logits) || !aligned4(state) || ((uintptr_t)token & 7u)) return BF16X_EARG;
+  hipLaunchKernelGGL(greedy_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, (int)vocab, token, state,
+                     history, (int)history_len);
+  return launch_status();
+}

@@ -1,0 +1,369 @@
+"""Llama-style decoder stack over BF16X linears: the caller of the hot path.
+
+The reference's harness (bench_fused_cpm5.py:27-57) loads a Hugging Face
+model, swaps its nn.Linears for Bf16xFused with deploy_bf16x_fused
+(bf16x_fused.py:232-263), then runs a KV-cache greedy loop with one
+`.item()` host sync per token.  Here the model is a seeded random-init
+Llama-style stack (no checkpoint is available), its linears are swapped by
+the same deploy_bf16x_fused (bfloat16x_amd.nn), and decoding runs on
+device-resident state:
+
+  * the next token, its position and the history live in device memory;
+    the decode step reads them there, so one step is a fixed launch
+    sequence captured once in a HIP graph (torch.cuda.CUDAGraph) and
+    replayed per token with no host synchronisation;
+  * the ops between the linears are the kernels of include/bf16x_llama.h:
+    per layer RMSNorm(+residual), qkv GEMV, RoPE + KV append, attention,
+    o GEMV, RMSNorm(+residual), gate_up GEMV, SwiGLU, down GEMV: 9 launches;
+  * q/k/v and gate/up are single fused linears ([q; k; v] and [gate; up]
+    rows), so batch-1 decode runs 4 GEMVs per layer.
+
+Shapes of the benchmark configuration (the defaults of LlamaConfig): 32
+layers, hidden 4096, FFN 14336 (SwiGLU), 32 query / 8 KV heads, head_dim 128,
+vocab 128256, RoPE theta 5e5, RMSNorm weights 1; all linear weights
+N(0, 0.02) in bf16; embedding and lm_head bf16 N(0, 0.02), not compressed
+(the reference's deploy skips "lm_head" and "embed").
+"""
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import torch
+from torch import nn
+
+from . import _lib
+
+__all__ = ["LlamaConfig", "LlamaStack", "LlamaRunner", "rope_table", "rmsnorm", "rope_kv", "attention",
+           "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
+
+NORM_ADD, NORM_STORE = 1, 2
+HEAD_DIM = 128
+
+
+@dataclasses.dataclass(frozen=True)
+class LlamaConfig:
+    n_layers: int = 32
+    hidden: int = 4096
+    ffn: int = 14336
+    n_heads: int = 32
+    n_kv_heads: int = 8
+    head_dim: int = HEAD_DIM
+    vocab: int = 128256
+    rope_theta: float = 5e5
+    eps: float = 1e-5
+
+    def __post_init__(self):
+        if self.head_dim != HEAD_DIM:
+            raise ValueError("head_dim must be 128")
+        if self.n_heads % self.n_kv_heads or self.n_heads * self.head_dim != self.hidden:
+            raise ValueError("n_heads * head_dim must equal hidden and n_kv_heads must divide n_heads")
+        if self.hidden % 32 or self.ffn % 32 or self.vocab % 8 or self.hidden > 8192:
+            raise ValueError("hidden, ffn must be multiples of 32 (hidden <= 8192), vocab of 8")
+
+    @property
+    def qkv_rows(self) -> int:
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+    def linear_shapes(self):
+        """(name, out_f, in_f) of one layer's linears."""
+        return [("qkv", self.qkv_rows, self.hidden), ("o", self.hidden, self.hidden),
+                ("gate_up", 2 * self.ffn, self.hidden), ("down", self.hidden, self.ffn)]
+
+    def linear_params(self) -> int:
+        return self.n_layers * sum(o * i for _, o, i in self.linear_shapes())
+
+
+# ---------------------------------------------------------------------------
+# thin wrappers of include/bf16x_llama.h (shapes are checked here: the
+# kernels trust the buffer sizes they are given)
+
+def _stream(t: torch.Tensor):
+    return _lib.stream_of(t.device)
+
+
+def _need(cond: bool, what: str):
+    if not cond:
+        raise ValueError(what)
+
+
+def _bf16_dev(t, name):
+    _need(isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.bfloat16 and t.is_contiguous(),
+          f"{name} must be a contiguous bf16 GPU tensor")
+
+
+def rmsnorm(x, weight, out, residual=None, row_idx=None, flags=0, eps=1e-5):
+    """out = RMSNorm(h) * weight with h = x (or x[row_idx], a gather) plus,
+    with NORM_ADD, the residual; NORM_STORE writes h back to the residual."""
+    n = weight.numel()
+    for t, nm in ((x, "x"), (weight, "weight"), (out, "out")):
+        _bf16_dev(t, nm)
+    _need(x.numel() % n == 0, "x is not a whole number of rows")
+    if row_idx is not None:
+        _need(row_idx.is_cuda and row_idx.dtype == torch.int64 and row_idx.is_contiguous(), "row_idx: int64 GPU")
+        rows = row_idx.numel()
+    else:
+        rows = x.numel() // n
+    _need(out.numel() >= rows * n, "out too small")
+    if flags:
+        _bf16_dev(residual, "residual")
+        _need(residual.numel() >= rows * n, "residual too small")
+    st = _lib.lib().bf16x_rmsnorm(x.data_ptr(), _lib.ptr(row_idx), x.numel() // n,
+                                  residual.data_ptr() if residual is not None else None, weight.data_ptr(),
+                                  out.data_ptr(), rows, n, float(eps), int(flags), _stream(x))
+    _lib.check(st, "bf16x_rmsnorm")
+
+
+def _check_pos(pos):
+    _need(pos.is_cuda and pos.dtype == torch.int32 and pos.numel() >= 1, "pos: int32 GPU tensor")
+
+
+def rope_kv(qkv, pos, cos_sin, n_heads, n_kv_heads, q_out, k_cache, v_cache):
+    """RoPE of the q/k heads of qkv [tokens, (H + 2 KV) * 128] at positions
+    pos[0] + t; q to q_out, k and v appended to the [KV, max_len, 128]
+    caches."""
+    for t, nm in ((qkv, "qkv"), (q_out, "q_out"), (k_cache, "k_cache"), (v_cache, "v_cache")):
+        _bf16_dev(t, nm)
+    _check_pos(pos)
+    row = (n_heads + 2 * n_kv_heads) * HEAD_DIM
+    _need(qkv.numel() % row == 0, "qkv is not a whole number of tokens")
+    tokens = qkv.numel() // row
+    max_len = k_cache.numel() // (n_kv_heads * HEAD_DIM)
+    _need(k_cache.numel() == max_len * n_kv_heads * HEAD_DIM and v_cache.numel() == k_cache.numel(), "cache shape")
+    _need(q_out.numel() >= tokens * n_heads * HEAD_DIM, "q_out too small")
+    _need(cos_sin.is_cuda and cos_sin.dtype == torch.float32 and cos_sin.numel() == max_len * HEAD_DIM,
+          "cos_sin must be fp32 [max_len, 64, 2] on the GPU")
+    st = _lib.lib().bf16x_rope_kv(qkv.data_ptr(), tokens, pos.data_ptr(), cos_sin.data_ptr(), n_heads, n_kv_heads,
+                                  HEAD_DIM, max_len, q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+                                  _stream(qkv))
+    _lib.check(st, "bf16x_rope_kv")
+
+
+def attention(q, k_cache, v_cache, pos, n_heads, n_kv_heads, out, scale=None, tokens=None):
+    """Causal GQA attention of `tokens` queries at positions pos[0] + t over
+    the caches; out [tokens, n_heads * 128]."""
+    for t, nm in ((q, "q"), (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out")):
+        _bf16_dev(t, nm)
+    _check_pos(pos)
+    if tokens is None:
+        tokens = q.numel() // (n_heads * HEAD_DIM)
+    max_len = k_cache.numel() // (n_kv_heads * HEAD_DIM)
+    _need(k_cache.numel() == max_len * n_kv_heads * HEAD_DIM and v_cache.numel() == k_cache.numel(), "cache shape")
+    _need(q.numel() >= tokens * n_heads * HEAD_DIM and out.numel() >= tokens * n_heads * HEAD_DIM, "q/out size")
+    scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    st = _lib.lib().bf16x_attention(q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), pos.data_ptr(), tokens,
+                                    n_heads, n_kv_heads, HEAD_DIM, max_len, float(scale), out.data_ptr(), _stream(q))
+    _lib.check(st, "bf16x_attention")
+
+
+def silu_mul(gate_up, out, ffn):
+    """out[t] = silu(gate_up[t, :ffn]) * gate_up[t, ffn:]."""
+    _bf16_dev(gate_up, "gate_up")
+    _bf16_dev(out, "out")
+    _need(gate_up.numel() % (2 * ffn) == 0, "gate_up is not a whole number of tokens")
+    tokens = gate_up.numel() // (2 * ffn)
+    _need(out.numel() >= tokens * ffn, "out too small")
+    st = _lib.lib().bf16x_silu_mul(gate_up.data_ptr(), tokens, ffn, out.data_ptr(), _stream(gate_up))
+    _lib.check(st, "bf16x_silu_mul")
+
+
+def greedy(logits, token, state, history):
+    """token[0] = argmax(logits); history[state[1]] = token; state += 1."""
+    _bf16_dev(logits, "logits")
+    _need(token.is_cuda and token.dtype == torch.int64 and token.numel() >= 1, "token: int64 GPU")
+    _need(state.is_cuda and state.dtype == torch.int32 and state.numel() >= 2, "state: int32[2] GPU")
+    _need(history.is_cuda and history.dtype == torch.int32, "history: int32 GPU")
+    st = _lib.lib().bf16x_greedy(logits.data_ptr(), logits.numel(), token.data_ptr(), state.data_ptr(),
+                                 history.data_ptr(), history.numel(), _stream(logits))
+    _lib.check(st, "bf16x_greedy")
+
+
+def rope_table(max_len: int, theta: float, device) -> torch.Tensor:
+    """fp32 [max_len, 64, 2] (cos, sin) of position x inverse frequency, the
+    Hugging Face Llama construction: inv_freq = 1 / theta^(2i/128) and the
+    angle product in fp32."""
+    inv = 1.0 / (theta ** (torch.arange(0, HEAD_DIM, 2, dtype=torch.int64).float() / HEAD_DIM))
+    ang = torch.outer(torch.arange(max_len, dtype=torch.float32), inv)
+    return torch.stack([ang.cos(), ang.sin()], dim=-1).contiguous().to(device)
+
+
+# ---------------------------------------------------------------------------
+# the model
+
+def _device(device):
+    if device is None:
+        if not torch.cuda.is_available():
+            raise RuntimeError("the Llama harness runs on the GPU only")
+        device = torch.device("cuda", torch.cuda.current_device())
+    return torch.device(device)
+
+
+def _linear(w: torch.Tensor) -> nn.Linear:
+    lin = nn.Linear(w.shape[1], w.shape[0], bias=False, device="meta")
+    lin.weight = nn.Parameter(w, requires_grad=False)
+    return lin
+
+
+class LlamaStack(nn.Module):
+    """Random-init Llama-style decoder stack (bf16 nn.Linears until
+    deploy_bf16x_fused replaces them).  Weights come from a device generator
+    seeded per tensor, so the model does not depend on construction order."""
+
+    def __init__(self, cfg: LlamaConfig = LlamaConfig(), device=None, seed: int = 0, std: float = 0.02):
+        super().__init__()
+        dev = _device(device)
+        self.cfg = cfg
+        g = torch.Generator(device=dev)
+
+        def rnd(shape, k):
+            g.manual_seed(seed * 1_000_003 + k)
+            return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std).to(torch.bfloat16)
+
+        ones = lambda: nn.Parameter(torch.ones(cfg.hidden, dtype=torch.bfloat16, device=dev), requires_grad=False)
+        self.embed = nn.Parameter(rnd((cfg.vocab, cfg.hidden), 1), requires_grad=False)
+        self.layers = nn.ModuleList()
+        for i in range(cfg.n_layers):
+            lay = nn.Module()
+            lay.attn_norm = ones()
+            lay.mlp_norm = ones()
+            for j, (name, o, n) in enumerate(cfg.linear_shapes()):
+                setattr(lay, name, _linear(rnd((o, n), 16 + 8 * i + j)))
+            self.layers.append(lay)
+        self.norm = ones()
+        self.lm_head = _linear(rnd((cfg.vocab, cfg.hidden), 2))
+
+    @property
+    def device(self):
+        return self.embed.device
+
+
+class LlamaRunner:
+    """Prefill + greedy decode over a LlamaStack whose linears are bf16
+    nn.Linear or BF16X modules (anything mapping [.., in] -> [.., out]).
+
+    Device state: `token` (int64 [1], the next input), `state` (int32 [2]:
+    position of `token`, number of tokens in `history`), `history` (int32
+    [max_new]).  prefill() fills the caches with the prompt and emits the
+    first token; each decode step consumes `token`, appends one token to the
+    history and advances the position."""
+
+    def __init__(self, model: LlamaStack, max_len: int, max_new: int, max_prompt: int | None = None):
+        cfg = model.cfg
+        self.model, self.cfg = model, cfg
+        dev = model.device
+        if max_len > 16384:
+            raise ValueError("max_len <= 16384 (attention scores are kept in LDS)")
+        self.max_len, self.max_new = int(max_len), int(max_new)
+        self.max_prompt = int(max_prompt if max_prompt is not None else max_len)
+        T = max(self.max_prompt, 1)
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        self.k_cache = torch.zeros(cfg.n_layers, cfg.n_kv_heads, self.max_len, HEAD_DIM, **bf)
+        self.v_cache = torch.zeros_like(self.k_cache)
+        self.cos_sin = rope_table(self.max_len, cfg.rope_theta, dev)
+        self.residual = torch.empty(T, cfg.hidden, **bf)
+        self.normed = torch.empty(T, cfg.hidden, **bf)
+        self.q = torch.empty(T, cfg.n_heads * HEAD_DIM, **bf)
+        self.attn = torch.empty(T, cfg.n_heads * HEAD_DIM, **bf)
+        self.act = torch.empty(T, cfg.ffn, **bf)
+        self.token = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.state = torch.zeros(2, dtype=torch.int32, device=dev)
+        self.history = torch.zeros(max(self.max_new, 1), dtype=torch.int32, device=dev)
+        self.zero_pos = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.logits = None
+        self.graph = None
+        self._graph_logits = None
+        self._prompt_len = 0
+
+    # one pass over the stack for `T` tokens starting at position pos[0]
+    def _layers(self, T: int, pos: torch.Tensor, ids: torch.Tensor):
+        cfg, m = self.cfg, self.model
+        H, KV = cfg.n_heads, cfg.n_kv_heads
+        one = T == 1
+
+        def rows(buf):                    # decode feeds 1-D rows: the linears take the GEMV path
+            return buf[0] if one else buf[:T]
+
+        prev = None
+        for i, lay in enumerate(m.layers):
+            if i == 0:
+                rmsnorm(m.embed, lay.attn_norm, self.normed, self.residual, row_idx=ids, flags=NORM_STORE,
+                        eps=cfg.eps)
+            else:
+                rmsnorm(prev, lay.attn_norm, self.normed, self.residual, flags=NORM_ADD | NORM_STORE, eps=cfg.eps)
+            qkv = lay.qkv(rows(self.normed))
+            rope_kv(qkv, pos, self.cos_sin, H, KV, self.q, self.k_cache[i], self.v_cache[i])
+            attention(self.q, self.k_cache[i], self.v_cache[i], pos, H, KV, self.attn, tokens=T)
+            o = lay.o(rows(self.attn))
+            rmsnorm(o, lay.mlp_norm, self.normed, self.residual, flags=NORM_ADD | NORM_STORE, eps=cfg.eps)
+            gu = lay.gate_up(rows(self.normed))
+            silu_mul(gu, self.act, cfg.ffn)
+            prev = lay.down(rows(self.act))
+        return prev
+
+    def _head(self, last_down: torch.Tensor, last_res: torch.Tensor):
+        rmsnorm(last_down, self.model.norm, self.normed, last_res, flags=NORM_ADD, eps=self.cfg.eps)
+        self.logits = self.model.lm_head(self.normed[0])
+        greedy(self.logits, self.token, self.state, self.history)
+
+    @torch.no_grad()
+    def prefill(self, ids: torch.Tensor) -> None:
+        """Run the prompt (int64 token ids on the device), emit the first
+        token: afterwards state = (len(ids), 1), history[0] = token."""
+        T = int(ids.numel())
+        if not (1 <= T <= self.max_prompt) or T + self.max_new > self.max_len:
+            raise ValueError(f"prompt of {T} tokens: need 1 <= T <= {self.max_prompt} and T + max_new <= max_len")
+        if ids.dtype != torch.int64 or not ids.is_cuda:
+            raise ValueError("ids must be int64 on the GPU")
+        ids = ids.reshape(-1).contiguous()
+        self.state.copy_(torch.tensor([T - 1, 0], dtype=torch.int32))
+        self._prompt_len = T
+        down = self._layers(T, self.zero_pos, ids)
+        self._head(down.reshape(T, -1)[T - 1], self.residual[T - 1])
+
+    @torch.no_grad()
+    def step(self) -> None:
+        """One eager decode step."""
+        down = self._layers(1, self.state, self.token)
+        self._head(down, self.residual[0])
+
+    @torch.no_grad()
+    def capture(self) -> None:
+        """Capture one decode step in a HIP graph.  Warms up with an eager step
+        first (library handles, plans); the warm-up advances the state, so
+        run prefill() again before decoding."""
+        s = torch.cuda.Stream(device=self.model.device)
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.step()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.step()
+        self.graph = g
+        self._graph_logits = self.logits      # lives in the graph's pool, rewritten by every replay
+
+    def decode(self, n_steps: int, graph: bool = True) -> None:
+        """n_steps decode steps, asynchronous (no host sync)."""
+        if graph and self.graph is None:
+            raise RuntimeError("capture() first")
+        for _ in range(int(n_steps)):
+            if graph:
+                self.graph.replay()
+                self.logits = self._graph_logits
+            else:
+                self.step()
+
+    def generate(self, ids: torch.Tensor, n_new: int, graph: bool = True) -> list:
+        """Greedy decode of n_new tokens after the prompt; the token ids."""
+        if not (1 <= n_new <= self.max_new):
+            raise ValueError(f"n_new must be in [1, {self.max_new}]")
+        self.prefill(ids)
+        self.decode(n_new - 1, graph=graph)
+        return self.history[:n_new].tolist()
+
+    def kv_bytes_per_step(self) -> int:
+        """K and V bytes the attention of one decode step reads at the mean
+        context length of a generation from the current prompt."""
+        ctx = self._prompt_len + self.max_new / 2
+        return int(2 * self.cfg.n_layers * self.cfg.n_kv_heads * ctx * HEAD_DIM * 2)

@@ -1,0 +1,82 @@
+/*
+ * bf16x_llama.h -- decoder-stack kernels of the Llama-style harness that
+ * drives the BF16X linears (libbf16x_hip.so, same library as bf16x_hip.h).
+ *
+ * None of these entry points has a counterpart in the reference's own code:
+ * the reference's harness (bench_fused_cpm5.py:27-57) runs the ops between the
+ * linears (RMSNorm, rotary embedding, KV cache, attention, SwiGLU, greedy
+ * argmax) through Hugging Face transformers modules in PyTorch.  They exist so
+ * that one decode step is a short, fixed sequence of launches that a HIP
+ * graph can capture, with the token position kept on the device.
+ *
+ * Conventions (as in bf16x_hip.h): device pointers, an explicit stream, an
+ * int status (0 ok, < 0 BF16X_E* invalid argument, > 0 hipError_t).
+ * Activations are bf16 (uint16 bits), row-major; arithmetic is fp32.
+ *
+ * Layouts
+ *  - qkv      [tokens][(n_heads + 2 n_kv_heads) * head_dim]: q heads, then k
+ *             heads, then v heads (one fused projection)
+ *  - q        [tokens][n_heads][head_dim]
+ *  - k/v cache [n_kv_heads][max_len][head_dim] per layer
+ *  - cos_sin  fp32 [max_len][head_dim / 2][2] (cos, sin) of position x
+ *             inverse frequency, rotate-half convention (pairs i, i + d/2)
+ *  - gate_up  [tokens][2 ffn]: gate columns, then up columns
+ *  - pos      int32 on the device: position of the first token of the call
+ *  - state    int32 [2] on the device: {position of the next token, number
+ *             of tokens written to history}
+ */
+#ifndef BF16X_LLAMA_H
+#define BF16X_LLAMA_H
+
+#include <stdint.h>
+
+#include "bf16x_hip.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* flags of bf16x_rmsnorm */
+enum { BF16X_NORM_ADD = 1, BF16X_NORM_STORE = 2 };
+
+/* RMSNorm of `rows` rows of n elements, with the residual stream folded in.
+ * Row r of the input is x[r] (or x[row_idx[r]], an embedding gather, when
+ * row_idx is not NULL; indices are clamped to [0, x_rows)).  With
+ * BF16X_NORM_ADD, h = bf16(x + residual[r]), else h = x; with
+ * BF16X_NORM_STORE, residual[r] = h.  out[r] = bf16(bf16(h * rsqrt(mean(h^2)
+ * + eps)) * weight): the two roundings of the Hugging Face LlamaRMSNorm.
+ * n % 8 == 0, n <= 8192; x, residual, weight, out 16-byte aligned. */
+int bf16x_rmsnorm(const uint16_t* x, const int64_t* row_idx, int64_t x_rows, uint16_t* residual,
+                  const uint16_t* weight, uint16_t* out, int64_t rows, int64_t n, float eps, int32_t flags,
+                  bf16x_stream_t stream);
+
+/* Rotary embedding of the q and k heads of `tokens` tokens at positions
+ * *pos + t, q written to q_out, rotated k and plain v appended to the caches
+ * at those positions (positions >= max_len are not written).  head_dim 128. */
+int bf16x_rope_kv(const uint16_t* qkv, int64_t tokens, const int32_t* pos, const float* cos_sin,
+                  int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t max_len,
+                  uint16_t* q_out, uint16_t* k_cache, uint16_t* v_cache, bf16x_stream_t stream);
+
+/* Causal grouped-query attention: query t (position *pos + t) of head h
+ * attends to keys 0 .. *pos + t of kv head h / (n_heads / n_kv_heads);
+ * softmax(scale q.k) v in fp32, out [tokens][n_heads * head_dim] bf16.
+ * head_dim 128, max_len <= 16384. */
+int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache, const int32_t* pos,
+                    int64_t tokens, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t max_len,
+                    float scale, uint16_t* out, bf16x_stream_t stream);
+
+/* SwiGLU: out[t][i] = bf16(bf16(silu(gate[t][i])) * up[t][i]).  ffn % 8 == 0,
+ * 16-byte aligned buffers. */
+int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t ffn, uint16_t* out, bf16x_stream_t stream);
+
+/* Greedy step: token[0] = argmax(logits[0 .. vocab)) (the first maximum),
+ * history[state[1]] = token[0] when state[1] < history_len, then state[1]++
+ * and state[0]++.  logits 16-byte aligned. */
+int bf16x_greedy(const uint16_t* logits, int64_t vocab, int64_t* token, int32_t* state, int32_t* history,
+                 int64_t history_len, bf16x_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BF16X_LLAMA_H */

@@ -1,0 +1,281 @@
+"""GPU tests of the Llama harness.
+
+Kernels (include/bf16x_llama.h) against plain torch fp32 references of the
+same ops on the same bf16 inputs; then a small stack end to end: prefill
+logits against an fp32 CPU forward of the same weights, decode steps against
+a prefill over the same tokens (KV cache and positions), the HIP-graph
+decode against eager steps over several replays, and the BF16X-deployed
+stack against the bf16 one on the same token path."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from bfloat16x_amd import llama
+from tests.test_gpu_dict import DEV
+
+pytestmark = pytest.mark.gpu
+
+BF_ULP = 2.0 ** -7          # a bf16 ulp is at most 2^-7 of the value (7 stored mantissa bits)
+
+
+@pytest.fixture(scope="module")
+def bx():
+    import bfloat16x_amd as m
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return m
+
+
+def rnd(shape, seed, scale=1.0):
+    return (torch.randn(shape, generator=torch.Generator().manual_seed(seed)) * scale).to(torch.bfloat16)
+
+
+def bf(t):
+    """fp32 -> bf16 -> fp32 (one round to nearest even)."""
+    return t.to(torch.bfloat16).float()
+
+
+def within_ulps(got, ref, ulps=1.0):
+    got, ref = got.float().cpu(), ref.float().cpu()
+    err = (got - ref).abs()
+    bound = ulps * BF_ULP * ref.abs() + 1e-30
+    assert bool((err <= bound).all()), float((err - bound).max())
+
+
+def norm_rel(y, r):
+    y, r = np.asarray(y, np.float64).reshape(-1), np.asarray(r, np.float64).reshape(-1)
+    return float(np.linalg.norm(y - r) / np.linalg.norm(r))
+
+
+# --------------------------------------------------------------------------- kernels
+
+@torch.no_grad()
+@pytest.mark.parametrize("n,rows", [(4096, 3), (512, 5), (8192, 1), (1536, 2)])
+def test_rmsnorm(bx, n, rows):
+    x, r, w = rnd((rows, n), 1), rnd((rows, n), 2), rnd(n, 3)
+    eps = 1e-5
+    h = bf(x.float() + r.float())
+    y = bf(h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps))
+    ref = bf(y * w.float())
+    res = r.to(DEV)
+    out = torch.empty(rows, n, dtype=torch.bfloat16, device=DEV)
+    llama.rmsnorm(x.to(DEV), w.to(DEV), out, res, flags=llama.NORM_ADD | llama.NORM_STORE, eps=eps)
+    assert torch.equal(res.cpu(), h.to(torch.bfloat16))            # the residual add is exact RNE
+    within_ulps(out, ref, 1.0)
+    # plain norm, no residual
+    y0 = bf(x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps))
+    llama.rmsnorm(x.to(DEV), w.to(DEV), out, eps=eps)
+    within_ulps(out, bf(y0 * w.float()), 1.0)
+
+
+@torch.no_grad()
+def test_rmsnorm_gather_store(bx):
+    table, w = rnd((100, 512), 4), rnd(512, 5)
+    ids = torch.tensor([7, 0, 99, 7, 42], dtype=torch.int64)
+    res = torch.zeros(5, 512, dtype=torch.bfloat16, device=DEV)
+    out = torch.empty(5, 512, dtype=torch.bfloat16, device=DEV)
+    llama.rmsnorm(table.to(DEV), w.to(DEV), out, res, row_idx=ids.to(DEV), flags=llama.NORM_STORE)
+    h = table[ids].float()
+    assert torch.equal(res.cpu(), table[ids])
+    within_ulps(out, bf(bf(h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-5)) * w.float()), 1.0)
+
+
+def rope_ref(x, cs, pos):
+    """x [T, heads, 128] fp32, rotate-half at positions pos + t."""
+    T = x.shape[0]
+    c = cs[pos:pos + T, :, 0][:, None, :]
+    s = cs[pos:pos + T, :, 1][:, None, :]
+    a, b = x[..., :64], x[..., 64:]
+    return torch.cat([a * c - b * s, b * c + a * s], dim=-1)
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("T,pos", [(1, 0), (1, 37), (9, 5), (40, 0)])
+def test_rope_kv(bx, T, pos):
+    H, KV, L = 8, 2, 48
+    qkv = rnd((T, (H + 2 * KV) * 128), 6)
+    cs = llama.rope_table(L, 5e5, "cpu")
+    kc = torch.zeros(KV, L, 128, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    q = torch.zeros(T, H * 128, dtype=torch.bfloat16, device=DEV)
+    llama.rope_kv(qkv.to(DEV), torch.tensor([pos], dtype=torch.int32, device=DEV), cs.to(DEV), H, KV, q, kc, vc)
+    x = qkv.float().view(T, H + 2 * KV, 128)
+    qr = rope_ref(x[:, :H], cs, pos)
+    kr = rope_ref(x[:, H:H + KV], cs, pos)
+    within_ulps(q.view(T, H, 128), bf(qr), 1.0)
+    within_ulps(kc[:, pos:pos + T].permute(1, 0, 2), bf(kr), 1.0)
+    assert torch.equal(vc[:, pos:pos + T].permute(1, 0, 2).cpu(), qkv.view(T, H + 2 * KV, 128)[:, H + KV:])
+    # nothing written outside [pos, pos + T)
+    keep = torch.ones(L, dtype=torch.bool)
+    keep[pos:pos + T] = False
+    assert not kc[:, keep.to(DEV)].any() and not vc[:, keep.to(DEV)].any()
+
+
+@torch.no_grad()
+def test_rope_kv_positions_past_the_cache_are_dropped(bx):
+    H, KV, L = 4, 2, 16
+    qkv = rnd((4, (H + 2 * KV) * 128), 7)
+    kc = torch.zeros(KV, L, 128, dtype=torch.bfloat16, device=DEV)
+    vc = torch.zeros_like(kc)
+    q = torch.zeros(4, H * 128, dtype=torch.bfloat16, device=DEV)
+    llama.rope_kv(qkv.to(DEV), torch.tensor([14], dtype=torch.int32, device=DEV),
+                  llama.rope_table(L, 5e5, DEV), H, KV, q, kc, vc)
+    assert kc[:, 14:].abs().sum() > 0 and not kc[:, :14].any()          # positions 16, 17 not written
+
+
+def attn_ref(q, kc, vc, pos, H, KV):
+    """q [T, H, 128], caches [KV, L, 128] fp32; query t sees keys 0..pos+t."""
+    T = q.shape[0]
+    out = torch.empty(T, H, 128)
+    for t in range(T):
+        n = pos + t + 1
+        for h in range(H):
+            kvh = h // (H // KV)
+            s = (kc[kvh, :n] @ q[t, h]) / math.sqrt(128)
+            p = torch.softmax(s.double(), 0).float()
+            out[t, h] = p @ vc[kvh, :n]
+    return out
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("T,pos,L", [(1, 0, 16), (1, 300, 640), (7, 10, 64), (3, 1021, 1024)])
+def test_attention(bx, T, pos, L):
+    H, KV = 8, 2
+    q = rnd((T, H, 128), 8)
+    kc, vc = rnd((KV, L, 128), 9), rnd((KV, L, 128), 10)
+    out = torch.empty(T, H * 128, dtype=torch.bfloat16, device=DEV)
+    llama.attention(q.to(DEV).view(T, H * 128), kc.to(DEV), vc.to(DEV),
+                    torch.tensor([pos], dtype=torch.int32, device=DEV), H, KV, out)
+    ref = attn_ref(q.float(), kc.float(), vc.float(), pos, H, KV)
+    err = (out.float().cpu().view(T, H, 128) - ref).abs()
+    # fp32 softmax and sums, one bf16 rounding of the output
+    assert float((err - (BF_ULP * ref.abs() + 1e-4)).max()) <= 0, float(err.max())
+
+
+@torch.no_grad()
+def test_silu_mul(bx):
+    T, F = 3, 1536
+    gu = rnd((T, 2 * F), 11, 3.0)
+    out = torch.empty(T, F, dtype=torch.bfloat16, device=DEV)
+    llama.silu_mul(gu.to(DEV), out, F)
+    g, u = gu[:, :F].float(), gu[:, F:].float()
+    ref = bf(bf(g * torch.sigmoid(g)) * u)
+    within_ulps(out, ref, 1.0)
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("V", [1000, 1003, 128256])
+def test_greedy(bx, V):
+    logits = rnd(V, 12)
+    logits[V // 3] = 9.0
+    logits[V - 1] = 9.0                                  # tie: the first index wins
+    tok = torch.zeros(1, dtype=torch.int64, device=DEV)
+    state = torch.tensor([50, 0], dtype=torch.int32, device=DEV)
+    hist = torch.full((2,), -1, dtype=torch.int32, device=DEV)
+    lg = logits.to(DEV)
+    for _ in range(3):                                   # the third call is past the history: not written
+        llama.greedy(lg, tok, state, hist)
+    assert int(tok) == V // 3 == int(torch.argmax(logits.float()))
+    assert hist.tolist() == [V // 3, V // 3] and state.tolist() == [53, 3]
+
+
+# --------------------------------------------------------------------------- the stack
+
+SMALL = llama.LlamaConfig(n_layers=2, hidden=512, ffn=1536, n_heads=4, n_kv_heads=2, vocab=1000)
+
+
+def rms(x, w, eps):
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+
+def ref_forward(W, cfg, ids):
+    """fp32 CPU forward of the same weights: logits of every position."""
+    H, KV, T = cfg.n_heads, cfg.n_kv_heads, len(ids)
+    cs = llama.rope_table(T, cfg.rope_theta, "cpu")
+    x = W["embed"][ids]
+    for lw in W["layers"]:
+        h = rms(x, lw["attn_norm"], cfg.eps)
+        qkv = (h @ lw["qkv"].T).view(T, H + 2 * KV, 128)
+        q, k, v = rope_ref(qkv[:, :H], cs, 0), rope_ref(qkv[:, H:H + KV], cs, 0), qkv[:, H + KV:]
+        a = attn_ref(q, k.permute(1, 0, 2), v.permute(1, 0, 2), 0, H, KV).reshape(T, -1)
+        x = x + a @ lw["o"].T
+        h = rms(x, lw["mlp_norm"], cfg.eps)
+        gu = h @ lw["gate_up"].T
+        g, u = gu[:, :cfg.ffn], gu[:, cfg.ffn:]
+        x = x + (g * torch.sigmoid(g) * u) @ lw["down"].T
+    return rms(x, W["norm"], cfg.eps) @ W["lm_head"].T
+
+
+def host_weights(model):
+    f = lambda t: t.detach().float().cpu()
+    return {"embed": f(model.embed), "norm": f(model.norm), "lm_head": f(model.lm_head.weight),
+            "layers": [{k: f(getattr(l, k).weight if k in ("qkv", "o", "gate_up", "down") else getattr(l, k))
+                        for k in ("attn_norm", "mlp_norm", "qkv", "o", "gate_up", "down")} for l in model.layers]}
+
+
+@pytest.fixture(scope="module")
+def small(bx):
+    """(bf16 model, BF16X-deployed copy, host weights, prompt)."""
+    m16 = llama.LlamaStack(SMALL, device=DEV, seed=3, std=0.05)
+    W = host_weights(m16)
+    mx = llama.LlamaStack(SMALL, device=DEV, seed=3, std=0.05)
+    total, n_el = bx.deploy_bf16x_fused(mx, verbose=False)
+    assert n_el == SMALL.linear_params() and isinstance(mx.layers[0].qkv, bx.Bf16xFused)
+    ids = torch.randint(0, SMALL.vocab, (20,), generator=torch.Generator().manual_seed(0))
+    return m16, mx, W, ids
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("which", ["bf16", "bf16x"])
+def test_prefill_logits_match_fp32_forward(small, which):
+    m16, mx, W, ids = small
+    r = llama.LlamaRunner(m16 if which == "bf16" else mx, max_len=64, max_new=8, max_prompt=32)
+    r.prefill(ids.to(DEV))
+    ref = ref_forward(W, SMALL, ids)[-1]
+    assert norm_rel(r.logits.float().cpu().numpy(), ref.numpy()) < 2e-2
+    assert int(r.token) == int(r.history[0]) and r.state.tolist() == [len(ids), 1]
+
+
+@torch.no_grad()
+def test_decode_steps_match_prefill_over_same_tokens(small):
+    _, mx, _, ids = small
+    r = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32)
+    toks = r.generate(ids.to(DEV), 6, graph=False)
+    last = r.logits.float().cpu().numpy()
+    full = torch.cat([ids, torch.tensor(toks[:-1])])              # the token path of the decode
+    r2 = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32)
+    r2.prefill(full.to(DEV))
+    assert norm_rel(last, r2.logits.float().cpu().numpy()) < 1e-2
+    assert int(r2.history[0]) == toks[-1]
+
+
+@torch.no_grad()
+def test_graph_decode_matches_eager_over_replays(small):
+    _, mx, _, ids = small
+    r = llama.LlamaRunner(mx, max_len=64, max_new=12, max_prompt=32)
+    eager = r.generate(ids.to(DEV), 12, graph=False)
+    eager_logits = r.logits.clone()
+    r.capture()
+    for rep in range(3):                                          # eager work and syncs between the replays
+        torch.cuda.synchronize()
+        got = r.generate(ids.to(DEV), 12, graph=True)
+        assert got == eager, (rep, got, eager)
+        assert torch.equal(r.logits, eager_logits)
+
+
+@torch.no_grad()
+def test_bf16x_stack_tracks_bf16_stack(small):
+    """Teacher-forced on the BF16X stack's own tokens, the bf16 stack's
+    logits agree at every step (the weights are bit-identical; only the
+    accumulation order of the products differs)."""
+    m16, mx, _, ids = small
+    rx = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32)
+    r16 = llama.LlamaRunner(m16, max_len=64, max_new=8, max_prompt=32)
+    rx.prefill(ids.to(DEV))
+    r16.prefill(ids.to(DEV))
+    for k in range(7):
+        assert norm_rel(rx.logits.float().cpu().numpy(), r16.logits.float().cpu().numpy()) < 1e-2, k
+        r16.token.copy_(rx.token)
+        rx.step()
+        r16.step()

@@ -1,6 +1,7 @@
 """CPU tests of libbf16x_hip.so: exports, the host encoder, the plan builder
 and argument validation of the GPU entry points (rejected before any launch)."""
 import ctypes
+import glob
 import os
 import re
 
@@ -14,19 +15,22 @@ from tests.conftest import ROOT, golden_dict_cases
 import bfloat16x_amd as bx
 from bfloat16x_amd import _lib
 
-HEADER = os.path.join(ROOT, "include", "bf16x_hip.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "*.h")))
 
 
 def header_functions():
-    src = open(HEADER).read()
-    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"\b(bf16x_[a-z0-9_]+)\s*\(", src)))
+    names = set()
+    for h in HEADERS:
+        src = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(bf16x_[a-z0-9_]+)\s*\(", src))
+    return sorted(names)
 
 
 def test_library_exports_every_header_function():
     lib = _lib.lib()
+    assert len(HEADERS) == 2
     names = header_functions()
-    assert len(names) >= 9
+    assert len(names) >= 23
     for n in names:
         assert hasattr(lib, n), n
         assert n in _lib.PROTOTYPES, f"{n} has no ctypes prototype"

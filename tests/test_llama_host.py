@@ -1,0 +1,81 @@
+"""CPU tests of the Llama harness: configuration checks, the rotary table
+against its closed form, and argument validation of the decoder-stack entry
+points (rejected before any launch)."""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from bfloat16x_amd import _lib, llama
+
+
+def test_config_defaults_are_the_benchmark_stack():
+    c = llama.LlamaConfig()
+    assert (c.n_layers, c.hidden, c.ffn, c.n_heads, c.n_kv_heads, c.head_dim, c.vocab) == \
+        (32, 4096, 14336, 32, 8, 128, 128256)
+    assert c.qkv_rows == 6144
+    # 32 x (6144 + 4096 + 28672) x 4096 + 32 x 4096 x 14336 linear weights (about 6.98e9)
+    assert c.linear_params() == 32 * (6144 * 4096 + 4096 * 4096 + 28672 * 4096 + 4096 * 14336) == 6_979_321_856
+
+
+@pytest.mark.parametrize("kw", [dict(head_dim=64, hidden=2048), dict(n_kv_heads=5), dict(hidden=4000),
+                                dict(vocab=1001)])
+def test_config_rejects_unsupported(kw):
+    with pytest.raises(ValueError):
+        llama.LlamaConfig(**kw)
+
+
+def test_rope_table_closed_form():
+    t = llama.rope_table(40, 5e5, "cpu").double().numpy()
+    assert t.shape == (40, 64, 2)
+    for p in (0, 1, 17, 39):
+        for i in (0, 1, 31, 63):
+            ang = p * 5e5 ** (-2 * i / 128)
+            assert abs(t[p, i, 0] - math.cos(ang)) < 1e-5 and abs(t[p, i, 1] - math.sin(ang)) < 1e-5
+    assert np.all(t[0, :, 0] == 1) and np.all(t[0, :, 1] == 0)
+
+
+def _call(name, *args):
+    return getattr(_lib.lib(), name)(*args)
+
+
+def test_entry_points_validate_before_launch():
+    # every call below is rejected by the host-side checks, so the pointers
+    # are never dereferenced; `p` is a 16-byte aligned host address
+    keep = ctypes.create_string_buffer(1 << 16)
+    p = ctypes.addressof(keep) + (-ctypes.addressof(keep)) % 16
+    # bad flags, bad n, misalignment, residual missing
+    assert _call("bf16x_rmsnorm", p, None, 0, None, p, p, 1, 64, 1e-5, 4, None) == _lib.EARG
+    assert _call("bf16x_rmsnorm", p, None, 0, None, p, p, 1, 60, 1e-5, 0, None) == _lib.ESHAPE
+    assert _call("bf16x_rmsnorm", p, None, 0, None, p, p, 1, 8200, 1e-5, 0, None) == _lib.ESHAPE
+    assert _call("bf16x_rmsnorm", p + 2, None, 0, None, p, p, 1, 64, 1e-5, 0, None) == _lib.EARG
+    assert _call("bf16x_rmsnorm", p, None, 0, None, p, p, 1, 64, 1e-5, 1, None) == _lib.EARG
+    assert _call("bf16x_rmsnorm", p, p, 0, p, p, p, 1, 64, 1e-5, 2, None) == _lib.EARG      # x_rows 0
+    # rope: head_dim, head ratio
+    assert _call("bf16x_rope_kv", p, 1, p, p, 32, 8, 64, 16, p, p, p, None) == _lib.ESHAPE
+    assert _call("bf16x_rope_kv", p, 1, p, p, 30, 8, 128, 16, p, p, p, None) == _lib.ESHAPE
+    assert _call("bf16x_rope_kv", None, 1, p, p, 32, 8, 128, 16, p, p, p, None) == _lib.EARG
+    # attention: max_len above the LDS bound
+    assert _call("bf16x_attention", p, p, p, p, 1, 32, 8, 128, 16385, 0.1, p, None) == _lib.ESHAPE
+    assert _call("bf16x_attention", p, p + 4, p, p, 1, 32, 8, 128, 16, 0.1, p, None) == _lib.EARG
+    # silu_mul: ffn % 8
+    assert _call("bf16x_silu_mul", p, 1, 12, p, None) == _lib.ESHAPE
+    # greedy: misaligned token, history without length
+    assert _call("bf16x_greedy", p, 8, p + 4, p, p, 1, None) == _lib.EARG
+    assert _call("bf16x_greedy", p, 8, p, p, None, 1, None) == _lib.EARG
+    assert _call("bf16x_greedy", p, 0, p, p, p, 1, None) == _lib.ESHAPE
+    # zero rows / tokens: nothing to launch
+    assert _call("bf16x_rmsnorm", p, None, 0, None, p, p, 0, 64, 1e-5, 0, None) == _lib.OK
+    assert _call("bf16x_silu_mul", p, 0, 16, p, None) == _lib.OK
+
+
+def test_wrappers_refuse_cpu_tensors():
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        llama.rmsnorm(x, torch.ones(64, dtype=torch.bfloat16), torch.empty_like(x))
+    with pytest.raises(ValueError):
+        llama.silu_mul(torch.zeros(2, 32, dtype=torch.bfloat16), torch.zeros(2, 16, dtype=torch.bfloat16), 16)
+    with pytest.raises(RuntimeError):
+        llama.LlamaStack(llama.LlamaConfig(n_layers=1, hidden=512, ffn=1024, n_heads=4, n_kv_heads=2, vocab=64))
