@@ -19,7 +19,10 @@ activation rows through the fused kernel ("fused") and the default dispatch
 torch bf16 F.linear on the decoded weight beside them; and configuration 5
 (GGUF half-block, 8192x28672 and 28672x8192, Student-t(3) x 0.015): fused
 decode+GEMV, decode, decode+GEMM at M = 512, clamped fraction and max abs
-reconstruction error.
+reconstruction error; and configuration 4 (random-init Llama-style stack,
+512-token prefill + 128 greedy tokens): tok/s of the BF16X-deployed stack
+and of the same stack in bf16, against the HBM ceiling of the bytes each
+token reads.
 Printed as one JSON line; diagnostics go to stderr.
 """
 from __future__ import annotations
@@ -160,6 +163,95 @@ def bench_gguf(bx, dev, stream) -> list:
     return out
 
 
+def bench_llama(bx, dev, prompt_len: int = 512, n_new: int = 128, reps: int = 2) -> dict:
+    """Configuration 4: random-init Llama-style stack (32 layers, hidden 4096,
+    FFN 14336, 32/8 heads, vocab 128256), 512-token prefill of uniform random
+    ids (seed 0), then greedy decode of 128 tokens at batch 1 (the prefill's
+    token + 127 decode steps, each a HIP-graph replay).  The same stack runs
+    first with its bf16 nn.Linears, then after deploy_bf16x_fused.  ms/token
+    is wall clock over the 127 steps between two synchronisations, as the
+    reference's harness times it (bench_fused_cpm5.py:37-44)."""
+    from bfloat16x_amd import llama
+    cfg = llama.LlamaConfig()
+    t = time.time()
+    model = llama.LlamaStack(cfg, device=dev, seed=0)
+    model16 = llama.LlamaStack(cfg, device=dev, seed=0)           # the same weights, kept in bf16
+    torch.cuda.synchronize()
+    log(f"llama: random init {time.time() - t:.1f}s")
+    ids = torch.randint(0, cfg.vocab, (prompt_len,), generator=torch.Generator().manual_seed(0)).to(dev)
+    head_bytes = 2 * cfg.vocab * cfg.hidden
+
+    def run(tag, m, linear_bytes):
+        r = llama.LlamaRunner(m, max_len=prompt_len + n_new, max_new=n_new, max_prompt=prompt_len)
+        r.prefill(ids)
+        r.capture()
+        pre = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            r.prefill(ids)
+            torch.cuda.synchronize()
+            pre.append(time.perf_counter() - t0)
+        dec = []
+        for _ in range(reps):
+            r.prefill(ids)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            r.decode(n_new - 1)
+            torch.cuda.synchronize()
+            dec.append((time.perf_counter() - t0) / (n_new - 1))
+        toks = r.history[:n_new].tolist()
+        ms_tok = min(dec) * 1e3
+        per_tok = linear_bytes + head_bytes + r.kv_bytes_per_step()
+        ceil = HBM_PEAK_GBS * 1e9 / per_tok
+        rec = {"tok_per_s": round(1e3 / ms_tok, 1), "ms_per_token": round(ms_tok, 4),
+               "prefill_ms": round(min(pre) * 1e3, 2), "prefill_tok_per_s": round(prompt_len / min(pre), 1),
+               "bytes_per_token": per_tok, "hbm_ceiling_tok_per_s": round(ceil, 1),
+               "frac_of_ceiling": round(1e3 / ms_tok / ceil, 4)}
+        log(f"llama {tag}: {rec}")
+        del r
+        return rec, toks
+
+    rec16, toks16 = run("bf16", model16, 2 * cfg.linear_params())
+    t = time.time()
+    total, n_el = bx.deploy_bf16x_fused(model, verbose=False)
+    torch.cuda.synchronize()
+    t_deploy = time.time() - t
+    alg = 0
+    for lay in model.layers:
+        for name, _, _ in cfg.linear_shapes():
+            mod = getattr(lay, name)
+            alg += 4 * (mod._sign.numel() + mod._mant.numel() + mod._delta.numel()) + mod._emax.numel() \
+                + 5 * mod._n_fix
+    torch.cuda.empty_cache()
+    recx, toksx = run("bf16x", model, alg)
+    prefix = next((i for i, (a, b) in enumerate(zip(toksx, toks16)) if a != b), n_new)
+    # teacher forcing: the bf16 stack fed the BF16X stack's tokens; the weights
+    # are bit-identical, so the logits differ only by accumulation order
+    r16 = llama.LlamaRunner(model16, max_len=prompt_len + n_new, max_new=n_new, max_prompt=prompt_len)
+    r16.prefill(ids)
+    agree, worst = 0, 0.0
+    for k in range(n_new):
+        agree += int(r16.token) == toksx[k]
+        if k + 1 < n_new:
+            r16.token.fill_(toksx[k])
+            r16.step()
+    # logits of the last step, both stacks on the same context
+    rx = llama.LlamaRunner(model, max_len=prompt_len + 2 * n_new, max_new=n_new, max_prompt=prompt_len + n_new)
+    rx.prefill(torch.cat([ids, torch.tensor(toksx[:-1], device=dev)]))
+    worst = float(((rx.logits.float() - r16.logits.float()).norm() / r16.logits.float().norm()).item())
+    del model, model16, r16, rx
+    torch.cuda.empty_cache()
+    return {"workload": "random-init Llama-style stack 32L/4096/14336/32q8kv/vocab 128256, "
+                        f"{prompt_len}-token prefill + {n_new} greedy tokens, batch 1, HIP-graph decode",
+            "bf16x": recx, "bf16": rec16, "speedup_vs_bf16": round(recx["tok_per_s"] / rec16["tok_per_s"], 3),
+            "deploy_s": round(t_deploy, 1), "packed_bytes_reference_accounting": total,
+            "bpw": round(total * 8 / n_el, 3),
+            "teacher_forced_argmax_agreement": f"{agree}/{n_new}",
+            "last_logits_norm_rel_vs_bf16": round(worst, 5),
+            "free_running_identical_prefix": prefix}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -168,6 +260,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=7168)
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF (configuration 5) lines")
+    ap.add_argument("--no-llama", action="store_true", help="skip the Llama-stack (configuration 4) line")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 2048],
@@ -286,11 +379,16 @@ def main():
         del xm
 
     # ---- configuration 5: GGUF half-block, 70B-layer shapes, Student-t(3) x 0.015
+    del copies, argv
+    torch.cuda.empty_cache()
     gguf_rec = None
     if not args.no_gguf:
-        del copies, argv
-        torch.cuda.empty_cache()
         gguf_rec = bench_gguf(bx, dev, stream)
+
+    # ---- configuration 4: Llama-style stack, tok/s
+    llama_rec = None
+    if not args.no_llama:
+        llama_rec = bench_llama(bx, dev)
 
     cpu = None
     if not args.no_cpu:
@@ -323,6 +421,7 @@ def main():
         "decode_exact_14336x4096": decode_rec,
         "gemm_14336x4096_exact": gemm_rec,
         "gguf_config5": gguf_rec,
+        "llama_config4": llama_rec,
     }
     print(json.dumps(rec), flush=True)
 

@@ -62,11 +62,13 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   const uint16_t* xp = x + xr * n;
   uint16_t* rp = res ? res + r * n : nullptr;
   float h[kNormChunks][8];
+  u32x4 wreg[kNormChunks];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < kNormChunks; ++c) {
     const int i = (c * 256 + (int)threadIdx.x) * 8;
     if (i < n) {
+      wreg[c] = *(const u32x4*)(w + i);       // issued with x / residual: one memory round trip fewer
       const u32x4 xv = *(const u32x4*)(xp + i);
       u32x4 rv = {0u, 0u, 0u, 0u};
       if (flags & BF16X_NORM_ADD) rv = *(const u32x4*)(rp + i);
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const uint16_t* __restrict
   for (int c = 0; c < kNormChunks; ++c) {
     const int i = (c * 256 + (int)threadIdx.x) * 8;
     if (i < n) {
-      const u32x4 wv = *(const u32x4*)(w + i);
+      const u32x4 wv = wreg[c];
       const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
       uint32_t o[4];
 #pragma unroll
@@ -227,6 +229,270 @@ __global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restri
 }
 
 // ---------------------------------------------------------------------------
+// Decode attention (one token) with the rotary embedding and the KV append
+// folded in, split over the keys: workgroup (g, s) serves the G query heads
+// of KV head g over key range s of S (the n = pos + 1 keys cut into S equal
+// ranges), so that the K and V rows of the whole context are read by S x KV
+// workgroups at once instead of KV.
+//   0. every workgroup rotates the group's q heads (kept in LDS as fp32 of the
+//      bf16-rounded value x scale) and the new k, takes the new v; workgroup
+//      s = 0 appends the new k / v row to the caches.  The new key (position
+//      p, the last of the range) is always used from LDS: a cache row written
+//      in this launch is never read back;
+//   1. four lanes per key, 32 dims each (4 dwordx4 of the 256-byte row), G
+//      partial dot products reduced over the four lanes (the rows of the
+//      first 64 keys, K and V, are loaded at entry, before step 0);
+//   2. max and exponentials per head over the range;
+//   3. P.V: wave w takes keys w, w + 4, ... of the range, lane l dims 2l, 2l+1,
+//      16 row loads issued before their FMAs; the 4 wave sums reduced in LDS;
+//   4. the range's (max, sum, unnormalised output) go to the workspace; the
+//      last workgroup of KV head g to finish (a device-scope counter per KV
+//      head, which that workgroup resets to zero) rescales and combines the
+//      S ranges and writes the output.
+// Same arithmetic as rope_kv_kernel followed by attention_kernel.
+constexpr int kDecMaxSplits = 32;
+
+template <int G>
+__global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t* __restrict__ qkv,
+                                                          const int32_t* __restrict__ pos,
+                                                          const float* __restrict__ cs, int H, int KV, int max_len,
+                                                          float scale, uint16_t* __restrict__ kc,
+                                                          uint16_t* __restrict__ vc, float* __restrict__ ws,
+                                                          uint32_t* __restrict__ cnt, uint16_t* __restrict__ out) {
+  extern __shared__ float lds[];          // scores [G][range]; later wave sums [4][G][128]
+  __shared__ float qs[G][128];
+  __shared__ float kp[128], vp[128];
+  __shared__ float red[G][4];
+  __shared__ float ml[kDecMaxSplits][G][2];
+  __shared__ int last;
+  const int g = blockIdx.x, sp = blockIdx.y, S = gridDim.y;
+  const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+  const int p = pos[0];
+  const bool cur = p >= 0 && p < max_len;                        // the new row fits in the cache
+  const int n_old = p < 0 ? 0 : (p > max_len ? max_len : p);     // cached keys 0 .. n_old - 1
+  const int n = n_old + (cur ? 1 : 0);
+  const int chunk = (n + S - 1) / S;
+  const int j0 = sp * chunk < n ? sp * chunk : n;
+  const int j1 = j0 + chunk < n ? j0 + chunk : n;
+  const int jc = j1 < n_old ? j1 : n_old;                        // end of the cached keys of the range
+  // The K and V rows of the first 64 keys of the range are loaded before
+  // anything else so that their latency overlaps the rotary step.
+  const int q4 = tid & 3;
+  const uint16_t* K = kc + (int64_t)g * max_len * 128;
+  const uint32_t* V = (const uint32_t*)(vc + (int64_t)g * max_len * 128);
+  u32x4 kraw[4];
+  uint32_t vraw[16];
+  auto load_k = [&](int base) {
+    const int j = base + (tid >> 2);
+    const u32x4* kr = (const u32x4*)(K + (int64_t)(j < jc ? j : 0) * 128 + 32 * q4);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kraw[c] = j < jc ? kr[c] : u32x4{0u, 0u, 0u, 0u};
+  };
+  auto load_v = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int j = base + 4 * u;
+      vraw[u] = j < jc ? V[(int64_t)j * 64 + lane] : 0u;
+    }
+  };
+  load_k(j0);
+  load_v(j0 + wv);
+  // 0. rotary embedding, KV append
+  {
+    const int pc = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
+    const float c = cs[((int64_t)pc * 64 + lane) * 2], sn = cs[((int64_t)pc * 64 + lane) * 2 + 1];
+    for (int hh = wv; hh < G + 2; hh += 4) {
+      const int head = hh < G ? g * G + hh : (hh == G ? H + g : H + KV + g);
+      const uint16_t* src = qkv + (int64_t)head * 128;
+      const uint16_t a16 = src[lane], b16 = src[lane + 64];
+      if (hh <= G) {
+        const float a = bfv(a16), b = bfv(b16);
+        const uint32_t ra = f32_to_bf16_rne(a * c - b * sn), rb = f32_to_bf16_rne(b * c + a * sn);
+        if (hh < G) {
+          qs[hh][lane] = bfv(ra) * scale;
+          qs[hh][lane + 64] = bfv(rb) * scale;
+        } else {
+          kp[lane] = bfv(ra);
+          kp[lane + 64] = bfv(rb);
+          if (cur && sp == 0) {
+            uint16_t* dst = kc + ((int64_t)g * max_len + p) * 128;
+            dst[lane] = (uint16_t)ra;
+            dst[lane + 64] = (uint16_t)rb;
+          }
+        }
+      } else {
+        vp[lane] = bfv(a16);
+        vp[lane + 64] = bfv(b16);
+        if (cur && sp == 0) {
+          uint16_t* dst = vc + ((int64_t)g * max_len + p) * 128;
+          dst[lane] = a16;
+          dst[lane + 64] = b16;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // 1. scores, four lanes per key
+  float mx[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) mx[h] = -INFINITY;
+  for (int base = j0; base < j1; base += 64) {
+    if (base != j0) load_k(base);                                // ranges longer than 64 keys
+    const int j = base + (tid >> 2);
+    float s[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) s[h] = 0.f;
+    if (j < j1) {
+      float kf[32];
+      if (j < n_old) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const u32x4 kv = kraw[c];
+          const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            kf[8 * c + 2 * e] = bf16lo_to_f32(kw[e]);
+            kf[8 * c + 2 * e + 1] = bf16hi_to_f32(kw[e]);
+          }
+        }
+      } else {                                                   // the new key (j == p)
+#pragma unroll
+        for (int e = 0; e < 32; ++e) kf[e] = kp[32 * q4 + e];
+      }
+#pragma unroll
+      for (int e = 0; e < 32; ++e)
+#pragma unroll
+        for (int h = 0; h < G; ++h) s[h] = fmaf(qs[h][32 * q4 + e], kf[e], s[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      s[h] += __shfl_xor(s[h], 1, 64);
+      s[h] += __shfl_xor(s[h], 2, 64);
+    }
+    if (j < j1 && q4 == 0) {
+#pragma unroll
+      for (int h = 0; h < G; ++h) {
+        lds[h * chunk + (j - j0)] = s[h];
+        mx[h] = fmaxf(mx[h], s[h]);
+      }
+    }
+  }
+  float M[G], L[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    float v = mx[h];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    if (lane == 0) red[h][wv] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h) M[h] = fmaxf(fmaxf(red[h][0], red[h][1]), fmaxf(red[h][2], red[h][3]));
+  __syncthreads();
+  // 2. exponentials and sums
+  float sum[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) sum[h] = 0.f;
+  for (int j = j0 + tid; j < j1; j += 256) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float e = __expf(lds[h * chunk + (j - j0)] - M[h]);
+      lds[h * chunk + (j - j0)] = e;
+      sum[h] += e;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float v = wave_sum(sum[h]);
+    if (lane == 0) red[h][wv] = v;
+  }
+  __syncthreads();                         // also publishes the exponentials
+#pragma unroll
+  for (int h = 0; h < G; ++h) L[h] = (red[h][0] + red[h][1]) + (red[h][2] + red[h][3]);
+  // 3. P.V
+  float acc[G][2];
+#pragma unroll
+  for (int h = 0; h < G; ++h) acc[h][0] = acc[h][1] = 0.f;
+  for (int base = j0 + wv; base < j1; base += 64) {
+    if (base != j0 + wv) load_v(base);                           // ranges longer than 64 keys
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int j = base + 4 * u;
+      if (j < j1) {
+        float v0 = bf16lo_to_f32(vraw[u]), v1 = bf16hi_to_f32(vraw[u]);
+        if (j >= n_old) {                                        // the new value row (j == p)
+          v0 = vp[2 * lane];
+          v1 = vp[2 * lane + 1];
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+          const float pr = lds[h * chunk + (j - j0)];
+          acc[h][0] = fmaf(pr, v0, acc[h][0]);
+          acc[h][1] = fmaf(pr, v1, acc[h][1]);
+        }
+      }
+    }
+  }
+  __syncthreads();                         // every wave is done with the exponentials
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    lds[(wv * G + h) * 128 + 2 * lane] = acc[h][0];
+    lds[(wv * G + h) * 128 + 2 * lane + 1] = acc[h][1];
+  }
+  __syncthreads();
+  // 4. this range's partial result, then the combine by the last workgroup
+  float* wo = ws + ((int64_t)g * S + sp) * G * 130;              // [G][128] outputs, [G][2] (max, sum)
+  for (int e = tid; e < G * 128; e += 256) {
+    const int h = e >> 7, d = e & 127;
+    wo[e] = (lds[(0 * G + h) * 128 + d] + lds[(1 * G + h) * 128 + d]) +
+            (lds[(2 * G + h) * 128 + d] + lds[(3 * G + h) * 128 + d]);
+  }
+  if (tid < G) {
+    float Mh = M[0], Lh = L[0];
+#pragma unroll
+    for (int k = 1; k < G; ++k)
+      if (tid == k) {
+        Mh = M[k];
+        Lh = L[k];
+      }
+    wo[G * 128 + 2 * tid] = Mh;
+    wo[G * 128 + 2 * tid + 1] = Lh;
+  }
+  // The barrier orders every thread's partial stores before thread 0's
+  // device-scope release fence and count; the last workgroup's thread 0
+  // fences (acquire) before the barrier that releases its readers.
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    last = atomicAdd(&cnt[g], 1u) == (uint32_t)(S - 1);
+    if (last) __threadfence();
+  }
+  __syncthreads();
+  if (!last) return;
+  const float* wg = ws + (int64_t)g * S * G * 130;
+  for (int e = tid; e < S * G; e += 256) {
+    const int k = e / G, h = e - k * G;
+    ml[k][h][0] = wg[(int64_t)k * G * 130 + G * 128 + 2 * h];
+    ml[k][h][1] = wg[(int64_t)k * G * 130 + G * 128 + 2 * h + 1];
+  }
+  __syncthreads();
+  for (int e = tid; e < G * 128; e += 256) {
+    const int h = e >> 7;
+    float Mall = -INFINITY;
+    for (int k = 0; k < S; ++k) Mall = fmaxf(Mall, ml[k][h][0]);
+    float o = 0.f, l = 0.f;
+    for (int k = 0; k < S; ++k) {
+      const float f = ml[k][h][1] > 0.f ? __expf(ml[k][h][0] - Mall) : 0.f;
+      o = fmaf(wg[(int64_t)k * G * 130 + e], f, o);
+      l = fmaf(ml[k][h][1], f, l);
+    }
+    out[(int64_t)g * G * 128 + e] = l > 0.f ? to_bf(o / l) : (uint16_t)0;
+  }
+  if (tid == 0) atomicExch(&cnt[g], 0u);
+}
+
+
+// ---------------------------------------------------------------------------
 // SwiGLU over 8 columns per thread.
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t T, int F,
                                                        uint16_t* __restrict__ out) {
@@ -343,6 +609,60 @@ extern "C" int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const
   hipLaunchKernelGGL(attention_kernel, dim3((unsigned)n_heads, (unsigned)tokens), dim3(256),
                      (size_t)max_len * sizeof(float), (hipStream_t)stream, q, k_cache, v_cache, pos, (int)n_heads,
                      (int)n_kv_heads, (int)max_len, scale, out);
+  return launch_status();
+}
+
+static int host_dec_splits(int64_t max_len) {
+  const int64_t s = (max_len + 63) / 64;
+  return (int)(s < 1 ? 1 : (s > kDecMaxSplits ? kDecMaxSplits : s));
+}
+
+extern "C" int64_t bf16x_attention_decode_lds(int64_t n_heads, int64_t n_kv_heads, int64_t max_len) {
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || max_len <= 0 || max_len > INT32_MAX / 8)
+    return -1;
+  const int64_t G = n_heads / n_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return -1;
+  const int64_t S = host_dec_splits(max_len);
+  const int64_t range = (max_len + S - 1) / S;
+  const int64_t bytes = 4 * std::max<int64_t>(G * range, 4 * G * 128);
+  return bytes <= 48 * 1024 ? bytes : -1;
+}
+
+extern "C" int64_t bf16x_attention_decode_workspace(int64_t n_heads, int64_t n_kv_heads, int64_t max_len) {
+  if (bf16x_attention_decode_lds(n_heads, n_kv_heads, max_len) < 0) return -1;
+  const int64_t G = n_heads / n_kv_heads;
+  // counters first (one per KV head, 256-byte aligned block), then the partial results
+  return 256 * ((4 * n_kv_heads + 255) / 256) + 4 * n_kv_heads * host_dec_splits(max_len) * G * 130;
+}
+
+extern "C" int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, const float* cos_sin, int64_t n_heads,
+                                      int64_t n_kv_heads, int64_t head_dim, int64_t max_len, float scale,
+                                      uint16_t* k_cache, uint16_t* v_cache, void* workspace, int64_t workspace_bytes,
+                                      uint16_t* out, bf16x_stream_t stream) {
+  if (!qkv || !pos || !cos_sin || !k_cache || !v_cache || !out || !workspace) return BF16X_EARG;
+  if (head_dim != 128 || n_kv_heads > 65535) return BF16X_ESHAPE;
+  const int64_t lds = bf16x_attention_decode_lds(n_heads, n_kv_heads, max_len);
+  if (lds < 0) return BF16X_ESHAPE;
+  if (workspace_bytes < bf16x_attention_decode_workspace(n_heads, n_kv_heads, max_len)) return BF16X_ECAPACITY;
+  if (!aligned16(k_cache) || !aligned16(workspace) || !aligned4(v_cache) || !aligned4(cos_sin) || !aligned2(qkv) ||
+      !aligned2(out))
+    return BF16X_EARG;
+  const int G = (int)(n_heads / n_kv_heads);
+  const int S = host_dec_splits(max_len);
+  uint32_t* cnt = (uint32_t*)workspace;
+  float* part = (float*)((char*)workspace + 256 * ((4 * n_kv_heads + 255) / 256));
+  hipStream_t st = (hipStream_t)stream;
+#define BF16X_DEC(GG)                                                                                            \
+  hipLaunchKernelGGL(attn_decode_kernel<GG>, dim3((unsigned)n_kv_heads, (unsigned)S), dim3(256), (size_t)lds, st, \
+                     qkv, pos, cos_sin, (int)n_heads, (int)n_kv_heads, (int)max_len, scale, k_cache, v_cache, part, \
+                     cnt, out)
+  switch (G) {
+    case 1: BF16X_DEC(1); break;
+    case 2: BF16X_DEC(2); break;
+    case 4: BF16X_DEC(4); break;
+    default: BF16X_DEC(8); break;
+  }
+#undef BF16X_DEC
   return launch_status();
 }
 

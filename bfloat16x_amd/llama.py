@@ -13,8 +13,9 @@ device-resident state:
     sequence captured once in a HIP graph (torch.cuda.CUDAGraph) and
     replayed per token with no host synchronisation;
   * the ops between the linears are the kernels of include/bf16x_llama.h:
-    per layer RMSNorm(+residual), qkv GEMV, RoPE + KV append, attention,
-    o GEMV, RMSNorm(+residual), gate_up GEMV, SwiGLU, down GEMV: 9 launches;
+    per layer RMSNorm(+residual), qkv GEMV, RoPE + KV append + attention
+    (one launch per token), o GEMV, RMSNorm(+residual), gate_up GEMV,
+    SwiGLU, down GEMV: 8 launches;
   * q/k/v and gate/up are single fused linears ([q; k; v] and [gate; up]
     rows), so batch-1 decode runs 4 GEMVs per layer.
 
@@ -35,7 +36,7 @@ from torch import nn
 from . import _lib
 
 __all__ = ["LlamaConfig", "LlamaStack", "LlamaRunner", "rope_table", "rmsnorm", "rope_kv", "attention",
-           "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
+           "attention_decode", "attention_decode_supported", "attention_decode_workspace", "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
 
 NORM_ADD, NORM_STORE = 1, 2
 HEAD_DIM = 128
@@ -156,6 +157,40 @@ def attention(q, k_cache, v_cache, pos, n_heads, n_kv_heads, out, scale=None, to
     _lib.check(st, "bf16x_attention")
 
 
+def attention_decode_supported(n_heads, n_kv_heads, max_len) -> bool:
+    return int(_lib.lib().bf16x_attention_decode_lds(n_heads, n_kv_heads, max_len)) >= 0
+
+
+def attention_decode_workspace(n_heads, n_kv_heads, max_len, device) -> torch.Tensor:
+    """Zeroed workspace of attention_decode (its counters must start at zero;
+    every call leaves them zero)."""
+    nbytes = int(_lib.lib().bf16x_attention_decode_workspace(n_heads, n_kv_heads, max_len))
+    _need(nbytes > 0, "attention_decode does not support this shape")
+    return torch.zeros(nbytes // 4 + 1, dtype=torch.int32, device=device)
+
+
+def attention_decode(qkv, pos, cos_sin, n_heads, n_kv_heads, k_cache, v_cache, out, workspace, scale=None):
+    """One decode token: rope_kv + attention (tokens = 1) in one launch, the
+    keys split over workgroups that combine through `workspace`
+    (attention_decode_workspace)."""
+    for t, nm in ((qkv, "qkv"), (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out")):
+        _bf16_dev(t, nm)
+    _check_pos(pos)
+    _need(qkv.numel() == (n_heads + 2 * n_kv_heads) * HEAD_DIM, "qkv must hold one token")
+    max_len = k_cache.numel() // (n_kv_heads * HEAD_DIM)
+    _need(k_cache.numel() == max_len * n_kv_heads * HEAD_DIM and v_cache.numel() == k_cache.numel(), "cache shape")
+    _need(out.numel() >= n_heads * HEAD_DIM, "out too small")
+    _need(cos_sin.is_cuda and cos_sin.dtype == torch.float32 and cos_sin.numel() == max_len * HEAD_DIM,
+          "cos_sin must be fp32 [max_len, 64, 2] on the GPU")
+    _need(workspace.is_cuda and workspace.is_contiguous(), "workspace must be a contiguous GPU tensor")
+    scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    st = _lib.lib().bf16x_attention_decode(qkv.data_ptr(), pos.data_ptr(), cos_sin.data_ptr(), n_heads, n_kv_heads,
+                                           HEAD_DIM, max_len, float(scale), k_cache.data_ptr(), v_cache.data_ptr(),
+                                           workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+                                           out.data_ptr(), _stream(qkv))
+    _lib.check(st, "bf16x_attention_decode")
+
+
 def silu_mul(gate_up, out, ffn):
     """out[t] = silu(gate_up[t, :ffn]) * gate_up[t, ffn:]."""
     _bf16_dev(gate_up, "gate_up")
@@ -272,6 +307,10 @@ class LlamaRunner:
         self.logits = None
         self.graph = None
         self._graph_logits = None
+        # one-token steps fold RoPE + KV append into one attention launch per KV head
+        self.fused_decode_attention = attention_decode_supported(cfg.n_heads, cfg.n_kv_heads, self.max_len)
+        self.dec_ws = (attention_decode_workspace(cfg.n_heads, cfg.n_kv_heads, self.max_len, dev)
+                       if self.fused_decode_attention else None)
         self._prompt_len = 0
 
     # one pass over the stack for `T` tokens starting at position pos[0]
@@ -291,8 +330,12 @@ class LlamaRunner:
             else:
                 rmsnorm(prev, lay.attn_norm, self.normed, self.residual, flags=NORM_ADD | NORM_STORE, eps=cfg.eps)
             qkv = lay.qkv(rows(self.normed))
-            rope_kv(qkv, pos, self.cos_sin, H, KV, self.q, self.k_cache[i], self.v_cache[i])
-            attention(self.q, self.k_cache[i], self.v_cache[i], pos, H, KV, self.attn, tokens=T)
+            if one and self.fused_decode_attention:
+                attention_decode(qkv, pos, self.cos_sin, H, KV, self.k_cache[i], self.v_cache[i], self.attn,
+                                 self.dec_ws)
+            else:
+                rope_kv(qkv, pos, self.cos_sin, H, KV, self.q, self.k_cache[i], self.v_cache[i])
+                attention(self.q, self.k_cache[i], self.v_cache[i], pos, H, KV, self.attn, tokens=T)
             o = lay.o(rows(self.attn))
             rmsnorm(o, lay.mlp_norm, self.normed, self.residual, flags=NORM_ADD | NORM_STORE, eps=cfg.eps)
             gu = lay.gate_up(rows(self.normed))

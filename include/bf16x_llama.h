@@ -65,6 +65,24 @@ int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
                     int64_t tokens, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t max_len,
                     float scale, uint16_t* out, bf16x_stream_t stream);
 
+/* One decode token (at position *pos) through rotary embedding, KV append and
+ * attention in one launch: bf16x_rope_kv followed by bf16x_attention with
+ * tokens = 1.  The keys are split into ranges served by separate workgroups
+ * whose partial results meet in `workspace` (bf16x_attention_decode_workspace
+ * bytes, 16-byte aligned).  The workspace starts with one counter per KV head
+ * that must be zero before the first call; every call leaves it zero, so the
+ * caller zeroes the workspace once when allocating it.  Calls sharing a
+ * workspace must not overlap.  qkv [(n_heads + 2 n_kv_heads) * 128],
+ * out [n_heads * 128].  bf16x_attention_decode_lds(...) gives the bytes of
+ * workgroup memory used, -1 when the shape is not supported (head ratio other
+ * than 1, 2, 4, 8, or max_len too long); the workspace query returns -1 then. */
+int64_t bf16x_attention_decode_lds(int64_t n_heads, int64_t n_kv_heads, int64_t max_len);
+int64_t bf16x_attention_decode_workspace(int64_t n_heads, int64_t n_kv_heads, int64_t max_len);
+int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, const float* cos_sin, int64_t n_heads,
+                           int64_t n_kv_heads, int64_t head_dim, int64_t max_len, float scale,
+                           uint16_t* k_cache, uint16_t* v_cache, void* workspace, int64_t workspace_bytes,
+                           uint16_t* out, bf16x_stream_t stream);
+
 /* SwiGLU: out[t][i] = bf16(bf16(silu(gate[t][i])) * up[t][i]).  ffn % 8 == 0,
  * 16-byte aligned buffers. */
 int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t ffn, uint16_t* out, bf16x_stream_t stream);

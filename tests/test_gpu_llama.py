@@ -36,10 +36,10 @@ def bf(t):
     return t.to(torch.bfloat16).float()
 
 
-def within_ulps(got, ref, ulps=1.0):
+def within_ulps(got, ref, ulps=1.0, floor=1e-30):
     got, ref = got.float().cpu(), ref.float().cpu()
     err = (got - ref).abs()
-    bound = ulps * BF_ULP * ref.abs() + 1e-30
+    bound = ulps * BF_ULP * ref.abs() + floor
     assert bool((err <= bound).all()), float((err - bound).max())
 
 
@@ -150,6 +150,39 @@ def test_attention(bx, T, pos, L):
     ref = attn_ref(q.float(), kc.float(), vc.float(), pos, H, KV)
     err = (out.float().cpu().view(T, H, 128) - ref).abs()
     # fp32 softmax and sums, one bf16 rounding of the output
+    assert float((err - (BF_ULP * ref.abs() + 1e-4)).max()) <= 0, float(err.max())
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("H,KV,pos,L", [(4, 4, 0, 16), (8, 4, 5, 64), (32, 8, 300, 640), (32, 8, 639, 640),
+                                        (16, 2, 100, 640), (8, 1, 31, 48), (32, 8, 3000, 4096),
+                                        (64, 8, 511, 1024), (32, 8, 1, 640)])
+def test_attention_decode_matches_two_launch_path(bx, H, KV, pos, L):
+    """The fused one-token kernel against rope_kv + attention on the same
+    inputs: the same cache rows and outputs (one bf16 rounding apart at
+    most), and the fp32 reference."""
+    assert llama.attention_decode_supported(H, KV, L)
+    qkv = rnd((H + 2 * KV) * 128, 13)
+    kc0, vc0 = rnd((KV, L, 128), 14), rnd((KV, L, 128), 15)
+    cs = llama.rope_table(L, 5e5, DEV)
+    p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    kA, vA, kB, vB = kc0.to(DEV), vc0.to(DEV), kc0.to(DEV), vc0.to(DEV)
+    q = torch.empty(H * 128, dtype=torch.bfloat16, device=DEV)
+    outA = torch.empty(H * 128, dtype=torch.bfloat16, device=DEV)
+    outB = torch.empty_like(outA)
+    llama.rope_kv(qkv.to(DEV), p, cs, H, KV, q, kA, vA)
+    llama.attention(q, kA, vA, p, H, KV, outA)
+    ws = llama.attention_decode_workspace(H, KV, L, DEV)
+    llama.attention_decode(qkv.to(DEV), p, cs, H, KV, kB, vB, outB, ws)
+    assert not ws[:KV].any()                                        # the counters are left at zero
+    assert torch.equal(vA, vB)
+    within_ulps(kB, kA, 1.0)
+    keep = torch.ones(L, dtype=torch.bool, device=DEV)
+    keep[pos] = False
+    assert torch.equal(kB[:, keep], kc0.to(DEV)[:, keep])           # only row `pos` written
+    within_ulps(outB, outA, 1.0, floor=1e-4)         # summation order differs: near-zero outputs
+    ref = attn_ref(q.float().cpu().view(1, H, 128), kA.float().cpu(), vA.float().cpu(), pos, H, KV)
+    err = (outB.float().cpu().view(1, H, 128) - ref).abs()
     assert float((err - (BF_ULP * ref.abs() + 1e-4)).max()) <= 0, float(err.max())
 
 

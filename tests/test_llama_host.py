@@ -60,6 +60,11 @@ def test_entry_points_validate_before_launch():
     # attention: max_len above the LDS bound
     assert _call("bf16x_attention", p, p, p, p, 1, 32, 8, 128, 16385, 0.1, p, None) == _lib.ESHAPE
     assert _call("bf16x_attention", p, p + 4, p, p, 1, 32, 8, 128, 16, 0.1, p, None) == _lib.EARG
+    # decode attention: unsupported head ratio, workspace too small
+    assert _call("bf16x_attention_decode_lds", 24, 8, 640) == -1
+    assert _call("bf16x_attention_decode_workspace", 32, 8, 640) > 0
+    assert _call("bf16x_attention_decode", p, p, p, 24, 8, 128, 640, 0.1, p, p, p, 1 << 20, p, None) == _lib.ESHAPE
+    assert _call("bf16x_attention_decode", p, p, p, 32, 8, 128, 640, 0.1, p, p, p, 64, p, None) == _lib.ECAPACITY
     # silu_mul: ffn % 8
     assert _call("bf16x_silu_mul", p, 1, 12, p, None) == _lib.ESHAPE
     # greedy: misaligned token, history without length
