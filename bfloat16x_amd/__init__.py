@@ -10,12 +10,16 @@ Call surface (mirrors the reference dfytensor/bfloat16x):
   Bf16xFused, deploy_bf16x_fused       bf16x_fused.py:149-263
   Bf16xGemmLinear, deploy_bf16x_gemm   bf16x_gemm_fused.py:154-242
   BF16XLinear                          opqk_linear.py:327-407
+  disk.pack_model_to_disk / replace_linears_from_packed / Bf16xStreamLinear
+                                       pack_to_disk.py:40-265 (bf16x-v1 files)
+  llama.LlamaStack / LlamaRunner       the caller harness (bench_fused_cpm5.py:27-57)
 All GPU work runs in the HIP library libbf16x_hip.so through its C ABI
-(include/bf16x_hip.h).
+(include/bf16x_hip.h, include/bf16x_llama.h).
 """
 from ._lib import Bf16xError, version
 from .codec import Bf16xPlan, bf16x_quantize, build_plan_host, stream_words
-from . import gguf
+from . import disk, gguf, llama
+from .disk import Bf16xStreamLinear, pack_model_to_disk, replace_linears_from_packed
 from .nn import BF16XLinear, Bf16xFused, Bf16xGemmLinear, deploy_bf16x_fused, deploy_bf16x_gemm
 from .ops import (bf16x_decode, bf16x_decode_triton, bf16x_fused_gemm, bf16x_fused_gemv, bf16x_gemm,
                   bf16x_gemv)
@@ -25,4 +29,5 @@ __all__ = [
     "Bf16xError", "Bf16xPlan", "bf16x_decode", "bf16x_decode_triton", "bf16x_fused_gemm", "bf16x_fused_gemv",
     "bf16x_gemm", "bf16x_gemv",
     "bf16x_quantize", "build_plan_host", "gguf", "stream_words", "version",
+    "disk", "llama", "Bf16xStreamLinear", "pack_model_to_disk", "replace_linears_from_packed",
 ]
