@@ -19,7 +19,8 @@ activation rows through the fused kernel ("fused") and the default dispatch
 torch bf16 F.linear on the decoded weight beside them; and configuration 5
 (GGUF half-block, 8192x28672 and 28672x8192, Student-t(3) x 0.015): fused
 decode+GEMV, decode, decode+GEMM at M = 512, clamped fraction and max abs
-reconstruction error; and configuration 4 (random-init Llama-style stack,
+reconstruction error, and the same GEMV / decode with the lossless side
+table (bits per weight, bit-exactness); and configuration 4 (random-init Llama-style stack,
 512-token prefill + 128 greedy tokens): tok/s of the BF16X-deployed stack
 and of the same stack in bf16, against the HBM ceiling of the bytes each
 token reads.
@@ -129,6 +130,8 @@ def bench_gguf(bx, dev, stream) -> list:
         w = (rng.standard_t(3, size=(out_f, in_f)) * 0.015).astype(np.float32)
         blocks = bx.gguf.quantize_blocks(w)
         wb = torch.from_numpy(bx.gguf.fp32_to_bf16_bits(w).view(np.int16)).to(dev).view(torch.bfloat16)
+        blob = bx.gguf.pack_ovf(w)                 # lossless side table (BF16X-L)
+        ovf = bx.gguf.device_ovf(blob, blocks, dev)
         del w
         copies = [bx.gguf.device_blocks(blocks, dev) for _ in range(2)]
         nbytes = blocks.size
@@ -145,6 +148,12 @@ def bench_gguf(bx, dev, stream) -> list:
         del dec_out
         xm = torch.randn(512, in_f, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
         sec_m = time_launches(lambda i: bx.gguf.gguf_gemm(xm, copies[i % 2], out_f, in_f), 10, 2, stream)
+        sec_lv = time_launches(lambda i: bx.gguf.gguf_gemv(x, copies[i % 2], out_f, in_f, ovf=ovf), 200, 20, stream)
+        dec_l = bx.gguf.gguf_decode(copies[0], out_f, in_f, ovf=ovf)
+        lossless_exact = bool(torch.equal(dec_l.view(torch.int16), wb.view(torch.int16)))
+        sec_ld = time_launches(lambda i: bx.gguf.gguf_decode(copies[i % 2], out_f, in_f, out=dec_l, ovf=ovf), 30, 4,
+                               stream)
+        del dec_l
         wcopies = [wb, wb.clone()]
         sec_bv = time_launches(lambda i: torch.nn.functional.linear(x.view(1, -1), wcopies[i % 2]), 100, 10, stream)
         del wcopies, wb, copies, xm
@@ -157,7 +166,13 @@ def bench_gguf(bx, dev, stream) -> list:
                "decode_us": round(sec_d * 1e6, 2),
                "gemm_M512_us": round(sec_m * 1e6, 2),
                "gemm_M512_tflops": round(2.0 * 512 * out_f * in_f / sec_m / 1e12, 1),
-               "clamped_fraction": round(clamped, 5), "max_abs_reconstruction_error": err}
+               "clamped_fraction": round(clamped, 5), "max_abs_reconstruction_error": err,
+               "lossless": {"table_bytes": len(blob), "entries": ovf.n_entries,
+                            "bpw": round((nbytes + len(blob)) * 8 / (out_f * in_f), 3),
+                            "decode_bit_exact": lossless_exact,
+                            "gemv_us": round(sec_lv * 1e6, 2),
+                            "gemv_GBps": round((vbytes + len(blob)) / sec_lv / 1e9, 1),
+                            "decode_us": round(sec_ld * 1e6, 2)}}
         log(f"gguf {ent}")
         out.append(ent)
     return out

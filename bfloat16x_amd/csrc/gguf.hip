@@ -32,9 +32,17 @@ __device__ __forceinline__ int chunk_slot(int a, int q) { return a * 64 + (((q +
 // decode: one wave per row, 64 blocks per pass, staged through LDS so that
 // each store instruction writes contiguous bytes (1 KB bf16, 2 KB fp32)
 // ---------------------------------------------------------------------------
-template <bool F32>
+// With OVF, the lossless side table (bf16x_gguf_block.py:96-113) is applied
+// in LDS before each pass is stored: row_off [out_f + 1] and entries
+// (column | bf16 bits << 16, sorted by row then column) as in the reference's
+// blob.  Entries are taken in column order with a per-row cursor: a pass reads
+// the next 64 entries of its row, writes those whose column falls in the
+// pass, and advances by their count (ballot).
+template <bool F32, bool OVF>
 __global__ __launch_bounds__(256) void gguf_decode_kernel(const uint8_t* __restrict__ blocks, int64_t out_f,
-                                                          int64_t in_f, void* __restrict__ out) {
+                                                          int64_t in_f, const uint32_t* __restrict__ ovf_off,
+                                                          const uint32_t* __restrict__ ovf_ent,
+                                                          void* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[4 * 4096];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -53,6 +61,11 @@ __global__ __launch_bounds__(256) void gguf_decode_kernel(const uint8_t* __restr
     const uint32_t a = (uint32_t)min((int64_t)c * 64 + lane, P - 1);
     load_gguf_raw(rs, skew + a * kBlockBytes, r);
   };
+  uint32_t ecur = 0, eend = 0;
+  if constexpr (OVF) {
+    ecur = ovf_off[row];
+    eend = ovf_off[row + 1];
+  }
   GgufRaw cur, nxt;
   load(0, cur);
   for (int c = 0; c < passes; ++c) {
@@ -71,6 +84,23 @@ __global__ __launch_bounds__(256) void gguf_decode_kernel(const uint8_t* __restr
     *(u32x4*)(buf + chunk_slot(lane, 3)) = u32x4{hi[4], hi[5], hi[6], hi[7]};
     const int64_t col0 = (int64_t)c * 2048;
     const int64_t nvalid = min((int64_t)2048, in_f - col0);
+    if constexpr (OVF) {
+      // same wave: these LDS writes land after the decoded values above
+      while (ecur < eend) {
+        const uint32_t e = ecur + (uint32_t)lane;
+        const uint32_t en = e < eend ? ovf_ent[e] : 0xFFFFFFFFu;
+        const uint32_t col = en & 0xFFFFu;
+        const bool here = e < eend && (int64_t)col >= col0 && (int64_t)col < col0 + nvalid;
+        if (here) {
+          const uint32_t k = col - (uint32_t)col0;
+          *(uint16_t*)(buf + chunk_slot((int)(k >> 5), (int)((k >> 3) & 3)) + (k & 7) * 2) = (uint16_t)(en >> 16);
+        }
+        // entries are sorted: those before the pass end are a prefix of the 64
+        const uint32_t taken = (uint32_t)__builtin_popcountll(__ballot(e < eend && (int64_t)col < col0 + nvalid));
+        ecur += taken;
+        if (taken < 64) break;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int e = 8 * lane + 512 * i;
@@ -109,10 +139,17 @@ __global__ __launch_bounds__(256) void x_pairs_kernel(const uint16_t* __restrict
 // Loads of the next pass are issued before the current one is used; lanes
 // past the row's end load its last block again and add nothing.
 // ---------------------------------------------------------------------------
-template <bool YF32>
+// With OVF, each row adds the side table's correction: an entry's element
+// decodes as the zero marker (exponent 0, the entry's sign and mantissa;
+// checked on the host when the table is attached), so it contributes
+// (exact - marker) * x[col].  The row's first 128 entries are loaded before
+// the main loop.
+template <bool YF32, bool OVF>
 __global__ __launch_bounds__(256) void gguf_gemv_kernel(const uint8_t* __restrict__ blocks,
                                                         const uint32_t* __restrict__ xp, int64_t out_f,
-                                                        int64_t in_f, void* __restrict__ y) {
+                                                        int64_t in_f, const uint32_t* __restrict__ ovf_off,
+                                                        const uint32_t* __restrict__ ovf_ent,
+                                                        void* __restrict__ y) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   // XCD-aware row order: consecutive rows on one XCD
@@ -137,6 +174,14 @@ __global__ __launch_bounds__(256) void gguf_gemv_kernel(const uint8_t* __restric
     for (int q = 0; q < 4; ++q) l.x[q] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(a * 64 + 16 * q), 0, 0);
   };
   float acc = 0.f;
+  uint32_t eb = 0, ee = 0, en0 = 0, en1 = 0;
+  if constexpr (OVF) {
+    eb = ovf_off[row];
+    ee = ovf_off[row + 1];
+    const uint32_t last = ee > 0 ? ee - 1 : 0;
+    en0 = ovf_ent[min(eb + (uint32_t)lane, last)];
+    en1 = ovf_ent[min(eb + 64u + (uint32_t)lane, last)];
+  }
   Ld cur, nxt;
   load(0, cur);
   for (int c = 0; c < passes; ++c) {
@@ -156,6 +201,21 @@ __global__ __launch_bounds__(256) void gguf_gemv_kernel(const uint8_t* __restric
     }
     acc += live ? s : 0.f;
     cur = nxt;
+  }
+  if constexpr (OVF) {
+    auto corr = [&](uint32_t en) -> float {
+      const uint32_t col = min(en & 0xFFFFu, (uint32_t)in_f - 1);
+      const uint32_t xw = xp[(col >> 5) * 16 + (col & 15)];
+      const float xv = (col & 16) ? bf16hi_to_f32(xw) : bf16lo_to_f32(xw);
+      const uint32_t b = en >> 16;
+      return (bf16lo_to_f32(b) - bf16lo_to_f32(b & 0x807Fu)) * xv;
+    };
+    float cs = 0.f;
+    const float c0 = corr(en0), c1 = corr(en1);
+    cs += (eb + (uint32_t)lane < ee) ? c0 : 0.f;
+    cs += (eb + 64u + (uint32_t)lane < ee) ? c1 : 0.f;
+    for (uint32_t e = eb + 128u + (uint32_t)lane; e < ee; e += 64) cs += corr(ovf_ent[e]);
+    acc += cs;
   }
   acc = wave_sum(acc);
   if (lane == 0) {
@@ -183,8 +243,16 @@ int check_gguf(const void* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f)
 
 }  // namespace
 
-extern "C" int bf16x_gguf_decode(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f, void* out,
-                                 int32_t out_dtype, bf16x_stream_t stream) {
+namespace {
+
+int check_ovf(const uint32_t* row_off, const uint32_t* entries, int64_t n_entries) {
+  if (!row_off || !entries || n_entries < 0 || n_entries > 0xFFFFFFFFll) return BF16X_EARG;
+  if (!aligned4(row_off) || !aligned4(entries)) return BF16X_EARG;
+  return BF16X_OK;
+}
+
+int gguf_decode_launch(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f, const uint32_t* ovf_off,
+                       const uint32_t* ovf_ent, void* out, int32_t out_dtype, hipStream_t st) {
   int rc = check_gguf(blocks, n_bytes, out_f, in_f);
   if (rc) return rc;
   if (!out) return BF16X_EARG;
@@ -192,19 +260,24 @@ extern "C" int bf16x_gguf_decode(const uint8_t* blocks, int64_t n_bytes, int64_t
   if (!aligned16(out) || !aligned4(blocks)) return BF16X_EARG;
   const int64_t grid = (out_f + 3) / 4;
   if (grid > INT32_MAX) return BF16X_ESHAPE;
-  hipStream_t st = (hipStream_t)stream;
-  if (out_dtype == BF16X_F32)
-    hipLaunchKernelGGL(gguf_decode_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, blocks, out_f, in_f, out);
-  else
-    hipLaunchKernelGGL(gguf_decode_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, blocks, out_f, in_f, out);
+  const dim3 g((unsigned)grid), b(256);
+  if (ovf_off) {
+    if (out_dtype == BF16X_F32)
+      hipLaunchKernelGGL((gguf_decode_kernel<true, true>), g, b, 0, st, blocks, out_f, in_f, ovf_off, ovf_ent, out);
+    else
+      hipLaunchKernelGGL((gguf_decode_kernel<false, true>), g, b, 0, st, blocks, out_f, in_f, ovf_off, ovf_ent, out);
+  } else {
+    if (out_dtype == BF16X_F32)
+      hipLaunchKernelGGL((gguf_decode_kernel<true, false>), g, b, 0, st, blocks, out_f, in_f, nullptr, nullptr, out);
+    else
+      hipLaunchKernelGGL((gguf_decode_kernel<false, false>), g, b, 0, st, blocks, out_f, in_f, nullptr, nullptr, out);
+  }
   return launch_status();
 }
 
-extern "C" int64_t bf16x_gguf_gemv_workspace(int64_t in_f) { return in_f > 0 ? in_f * 2 : 0; }
-
-extern "C" int bf16x_gguf_gemv(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes, int64_t out_f,
-                               int64_t in_f, void* y, int32_t y_dtype, void* workspace, int64_t workspace_bytes,
-                               bf16x_stream_t stream) {
+int gguf_gemv_launch(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes, int64_t out_f,
+                     int64_t in_f, const uint32_t* ovf_off, const uint32_t* ovf_ent, void* y, int32_t y_dtype,
+                     void* workspace, int64_t workspace_bytes, hipStream_t st) {
   int rc = check_gguf(blocks, n_bytes, out_f, in_f);
   if (rc) return rc;
   if (!x || !y || !workspace) return BF16X_EARG;
@@ -213,13 +286,54 @@ extern "C" int bf16x_gguf_gemv(const void* x, int32_t x_dtype, const uint8_t* bl
   if (!aligned2(x) || !aligned16(workspace) || !aligned4(blocks) || !aligned4(y)) return BF16X_EARG;
   const int64_t grid = (out_f + 3) / 4;
   if (grid > INT32_MAX) return BF16X_ESHAPE;
-  hipStream_t st = (hipStream_t)stream;
   uint32_t* xp = (uint32_t*)workspace;
   hipLaunchKernelGGL(x_pairs_kernel, dim3((unsigned)((in_f / 2 + 255) / 256)), dim3(256), 0, st, (const uint16_t*)x,
                      in_f, xp);
-  if (y_dtype == BF16X_F32)
-    hipLaunchKernelGGL(gguf_gemv_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, blocks, xp, out_f, in_f, y);
-  else
-    hipLaunchKernelGGL(gguf_gemv_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, blocks, xp, out_f, in_f, y);
+  const dim3 g((unsigned)grid), b(256);
+  if (ovf_off) {
+    if (y_dtype == BF16X_F32)
+      hipLaunchKernelGGL((gguf_gemv_kernel<true, true>), g, b, 0, st, blocks, xp, out_f, in_f, ovf_off, ovf_ent, y);
+    else
+      hipLaunchKernelGGL((gguf_gemv_kernel<false, true>), g, b, 0, st, blocks, xp, out_f, in_f, ovf_off, ovf_ent, y);
+  } else {
+    if (y_dtype == BF16X_F32)
+      hipLaunchKernelGGL((gguf_gemv_kernel<true, false>), g, b, 0, st, blocks, xp, out_f, in_f, nullptr, nullptr, y);
+    else
+      hipLaunchKernelGGL((gguf_gemv_kernel<false, false>), g, b, 0, st, blocks, xp, out_f, in_f, nullptr, nullptr, y);
+  }
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" int bf16x_gguf_decode(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f, void* out,
+                                 int32_t out_dtype, bf16x_stream_t stream) {
+  return gguf_decode_launch(blocks, n_bytes, out_f, in_f, nullptr, nullptr, out, out_dtype, (hipStream_t)stream);
+}
+
+extern "C" int bf16x_gguf_decode_lossless(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f,
+                                          const uint32_t* row_off, const uint32_t* entries, int64_t n_entries,
+                                          void* out, int32_t out_dtype, bf16x_stream_t stream) {
+  const int rc = check_ovf(row_off, entries, n_entries);
+  if (rc) return rc;
+  return gguf_decode_launch(blocks, n_bytes, out_f, in_f, row_off, entries, out, out_dtype, (hipStream_t)stream);
+}
+
+extern "C" int64_t bf16x_gguf_gemv_workspace(int64_t in_f) { return in_f > 0 ? in_f * 2 : 0; }
+
+extern "C" int bf16x_gguf_gemv(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes, int64_t out_f,
+                               int64_t in_f, void* y, int32_t y_dtype, void* workspace, int64_t workspace_bytes,
+                               bf16x_stream_t stream) {
+  return gguf_gemv_launch(x, x_dtype, blocks, n_bytes, out_f, in_f, nullptr, nullptr, y, y_dtype, workspace,
+                          workspace_bytes, (hipStream_t)stream);
+}
+
+extern "C" int bf16x_gguf_gemv_lossless(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes,
+                                        int64_t out_f, int64_t in_f, const uint32_t* row_off,
+                                        const uint32_t* entries, int64_t n_entries, void* y, int32_t y_dtype,
+                                        void* workspace, int64_t workspace_bytes, bf16x_stream_t stream) {
+  const int rc = check_ovf(row_off, entries, n_entries);
+  if (rc) return rc;
+  return gguf_gemv_launch(x, x_dtype, blocks, n_bytes, out_f, in_f, row_off, entries, y, y_dtype, workspace,
+                          workspace_bytes, (hipStream_t)stream);
 }

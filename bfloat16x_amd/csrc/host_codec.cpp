@@ -285,3 +285,95 @@ extern "C" int bf16x_gguf_quantize_host(const uint16_t* bits, int64_t n_blocks, 
   });
   return BF16X_OK;
 }
+
+// ---------------------------------------------------------------------------
+// GGUF lossless side table (bf16x_gguf_block.py:96-185): the elements the
+// half-block quantizer turns into the zero marker although they are not
+// +-0: exponent delta >= 7 below the half-block max floored at 7 (:121-128).
+// Entries are (column | bf16 bits << 16), the little-endian reading of the
+// reference's {u16 col, u16 bf16_bits} pairs, sorted by row then column.
+namespace {
+inline bool gguf_ovf_elem(const uint16_t* blk, int j, const uint32_t emax[2]) {
+  const uint32_t ex = (blk[j] >> 7) & 0xFF;
+  return emax[j >> 4] - ex >= 7 && (blk[j] & 0x7FFF) != 0;
+}
+inline void gguf_block_emax(const uint16_t* blk, uint32_t emax[2]) {
+  emax[0] = emax[1] = 7u;
+  for (int j = 0; j < 32; ++j) emax[j >> 4] = std::max(emax[j >> 4], (uint32_t)((blk[j] >> 7) & 0xFF));
+}
+}  // namespace
+
+extern "C" int bf16x_gguf_ovf_pack_host(const uint16_t* bits, int64_t rows, int64_t cols, uint32_t* row_off,
+                                        uint32_t* entries, int64_t cap, int64_t* n_entries, int32_t n_threads) {
+  if (rows < 0 || cols <= 0 || cols % 32 != 0 || cols > 65536 || !n_entries) return BF16X_EARG;
+  if (rows > 0 && (!bits || !row_off)) return BF16X_EARG;
+  if (rows * cols > ((int64_t)1 << 40)) return BF16X_ESHAPE;
+  const int nth = host_threads(n_threads);
+  std::vector<int64_t> cnt(rows + 1, 0);
+  parallel_for(rows, nth, [&](int64_t b, int64_t e) {
+    for (int64_t r = b; r < e; ++r) {
+      int64_t c = 0;
+      for (int64_t k = 0; k < cols; k += 32) {
+        const uint16_t* blk = bits + r * cols + k;
+        uint32_t emax[2];
+        gguf_block_emax(blk, emax);
+        for (int j = 0; j < 32; ++j) c += gguf_ovf_elem(blk, j, emax);
+      }
+      cnt[r + 1] = c;
+    }
+  });
+  for (int64_t r = 0; r < rows; ++r) cnt[r + 1] += cnt[r];
+  *n_entries = cnt[rows];
+  if (cnt[rows] > 0xFFFFFFFFll) return BF16X_ESHAPE;
+  for (int64_t r = 0; r <= rows; ++r) row_off[r] = (uint32_t)cnt[r];
+  if (cnt[rows] > cap) return BF16X_ECAPACITY;
+  if (cnt[rows] > 0 && !entries) return BF16X_EARG;
+  parallel_for(rows, nth, [&](int64_t b, int64_t e) {
+    for (int64_t r = b; r < e; ++r) {
+      int64_t o = cnt[r];
+      for (int64_t k = 0; k < cols; k += 32) {
+        const uint16_t* blk = bits + r * cols + k;
+        uint32_t emax[2];
+        gguf_block_emax(blk, emax);
+        for (int j = 0; j < 32; ++j)
+          if (gguf_ovf_elem(blk, j, emax)) entries[o++] = (uint32_t)(k + j) | ((uint32_t)blk[j] << 16);
+      }
+    }
+  });
+  return BF16X_OK;
+}
+
+extern "C" int bf16x_gguf_ovf_check_host(const uint8_t* blocks, int64_t n_bytes, int64_t rows, int64_t cols,
+                                         const uint32_t* row_off, const uint32_t* entries, int64_t n_entries) {
+  if (rows <= 0 || cols <= 0 || cols % 32 != 0 || cols > 65536 || n_entries < 0) return BF16X_EARG;
+  if (!blocks || !row_off || (n_entries > 0 && !entries)) return BF16X_EARG;
+  const int64_t per_row = cols / 32 * 46;
+  if (n_bytes < rows * per_row) return BF16X_ESTREAM_LEN;
+  if (row_off[0] != 0 || (int64_t)row_off[rows] != n_entries) return BF16X_ETABLE;
+  for (int64_t r = 0; r < rows; ++r) {
+    if (row_off[r + 1] < row_off[r]) return BF16X_ETABLE;
+    int64_t prev = -1;
+    for (uint32_t e = row_off[r]; e < row_off[r + 1]; ++e) {
+      const int64_t col = entries[e] & 0xFFFF;
+      const uint32_t b16 = entries[e] >> 16;
+      if (col <= prev || col >= cols) return BF16X_ETABLE;   // sorted, unique, in range
+      prev = col;
+      // the element must decode as the zero marker (code 7) with the entry's
+      // sign and mantissa: the consumers correct by (exact - marker value)
+      const uint8_t* blk = blocks + r * per_row + (col / 32) * 46;
+      const int j = (int)(col % 32);
+      uint32_t sign, mw[7], dw[3];
+      memcpy(&sign, blk + 2, 4);
+      memcpy(mw, blk + 6, 28);
+      memcpy(dw, blk + 34, 12);
+      const uint64_t db = 3 * (uint64_t)j, mb = 7 * (uint64_t)j;
+      const uint64_t dpair = ((uint64_t)dw[std::min<uint64_t>((db >> 5) + 1, 2)] << 32) | dw[db >> 5];
+      const uint32_t code = (uint32_t)(dpair >> (db & 31)) & 7u;
+      const uint64_t mpair = ((uint64_t)mw[std::min<uint64_t>((mb >> 5) + 1, 6)] << 32) | mw[mb >> 5];
+      const uint32_t mant = (uint32_t)(mpair >> (mb & 31)) & 0x7Fu;
+      const uint32_t sgn = (sign >> j) & 1u;
+      if (code != 7u || mant != (b16 & 0x7Fu) || sgn != (b16 >> 15)) return BF16X_ETABLE;
+    }
+  }
+  return BF16X_OK;
+}

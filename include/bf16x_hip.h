@@ -212,6 +212,41 @@ int bf16x_gguf_gemv(const void* x, int32_t x_dtype, const uint8_t* blocks, int64
                     int64_t out_f, int64_t in_f, void* y, int32_t y_dtype,
                     void* workspace, int64_t workspace_bytes, bf16x_stream_t stream);
 
+/* GGUF lossless side table (bf16x_gguf_block.py:96-193).  The table of a
+ * weight [rows, cols] is the reference's blob without its 8-byte header:
+ *   row_off uint32 [rows + 1]   entry index where each row starts
+ *   entries uint32 [n_entries]  column | bf16 bits << 16 (the reference's
+ *                               {u16 col, u16 bf16_bits}, little endian),
+ *                               sorted by row then column
+ * holding every element the half-block quantizer turns into the zero marker
+ * although it is not +-0 (exponent delta >= 7, :121-128).
+ * bf16x_gguf_ovf_pack_host -> pack_ovf (:131-148), host; row_off is always
+ * filled and *n_entries set, BF16X_ECAPACITY if cap is too small.  cols <= 65536.
+ * bf16x_gguf_ovf_check_host: validates a table against its blocks (offsets
+ * monotone and consistent, columns strictly increasing and in range, and each
+ * entry on a zero-marker element with the entry's sign and mantissa), the
+ * condition under which the device consumers below are exact.  Host. */
+int bf16x_gguf_ovf_pack_host(const uint16_t* bits, int64_t rows, int64_t cols, uint32_t* row_off,
+                             uint32_t* entries, int64_t cap, int64_t* n_entries, int32_t n_threads);
+int bf16x_gguf_ovf_check_host(const uint8_t* blocks, int64_t n_bytes, int64_t rows, int64_t cols,
+                              const uint32_t* row_off, const uint32_t* entries, int64_t n_entries);
+
+/* bf16x_gguf_decode with the table applied (dequantize_lossless,
+ * bf16x_gguf_block.py:174-178): the original bf16 bits of every element.
+ * Device; row_off / entries device pointers (entries: at least one word). */
+int bf16x_gguf_decode_lossless(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, int64_t in_f,
+                               const uint32_t* row_off, const uint32_t* entries, int64_t n_entries,
+                               void* out, int32_t out_dtype, bf16x_stream_t stream);
+
+/* bf16x_gguf_gemv over the lossless weight: each row adds (exact - marker)
+ * x[col] for its table entries (the sparse correction of the reference's
+ * llama.cpp path, README.md:303-312).  The table must pass
+ * bf16x_gguf_ovf_check_host against the same blocks.  Device. */
+int bf16x_gguf_gemv_lossless(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes,
+                             int64_t out_f, int64_t in_f, const uint32_t* row_off, const uint32_t* entries,
+                             int64_t n_entries, void* y, int32_t y_dtype, void* workspace,
+                             int64_t workspace_bytes, bf16x_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,6 +14,16 @@ bf16 conversion for finite inputs and against golden vectors written by the
 reference for NaN/inf inputs; the block layout against hand-built
 known-answer blocks; the decode against the reference self-test invariants
 (bf16x_gguf_block.py:219-228) and golden vectors from the reference.
+
+Lossless side table (bf16x_gguf_block.py:96-185): ``ovf_mask_bits``,
+``pack_ovf_bits``, ``unpack_ovf``, ``apply_ovf_bits``,
+``dequantize_lossless_bits``.  Pinning (tests/test_gguf_ovf_host.py): the mask
+against an element-by-element brute force and hand-built blocks (delta 6 / 7,
++-0, denormals, the emax floor at 7); the blob against its header and offset
+invariants; the whole table by the lossless round trip (every element of
+the reference's self-test weights, :203-207, decodes to its original bits)
+together with minimality (no entry on an element the plain decode already
+returns exactly).
 """
 from __future__ import annotations
 
@@ -100,3 +110,77 @@ def student_t_weights(rows: int, cols: int, seed: int = 0) -> np.ndarray:
     """Configuration weights: Student-t(df=3) x 0.015, float32."""
     rng = np.random.default_rng(seed)
     return (rng.standard_t(3, size=(rows, cols)) * 0.015).astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# lossless side table (bf16x_gguf_block.py:96-185)
+# --------------------------------------------------------------------------
+OVF_HDR_BYTES = 8
+
+
+def ovf_mask_bits(bits: np.ndarray) -> np.ndarray:
+    """bf16 bits [rows, cols] -> bool mask of the elements the quantizer
+    clamps to the zero marker although they are not +-0: exponent delta >= 7
+    below the half-block max floored at 7 (bf16x_gguf_block.py:121-128)."""
+    b = np.asarray(bits, dtype=np.uint16)
+    rows, cols = b.shape
+    expo = ((b >> 7) & 0xFF).astype(np.int32).reshape(rows, cols // QK, 2, 16)
+    emax = np.maximum(expo.max(axis=-1, keepdims=True), 7)
+    delta = (emax - expo).reshape(rows, cols)
+    return (delta >= 7) & ((b & 0x7FFF) != 0)
+
+
+def ovf_mask_bruteforce(bits: np.ndarray) -> np.ndarray:
+    """The same mask element by element with Python loops (tiny inputs)."""
+    b = np.asarray(bits, dtype=np.uint16)
+    rows, cols = b.shape
+    out = np.zeros((rows, cols), dtype=bool)
+    for r in range(rows):
+        for c in range(cols):
+            h0 = (c // 16) * 16
+            emax = max(7, max(int((int(b[r, k]) >> 7) & 0xFF) for k in range(h0, h0 + 16)))
+            e = (int(b[r, c]) >> 7) & 0xFF
+            out[r, c] = (emax - e >= 7) and (int(b[r, c]) & 0x7FFF) != 0
+    return out
+
+
+def pack_ovf_bits(bits: np.ndarray) -> bytes:
+    """bf16 bits [rows, cols] -> the serialized table: u32 n_rows, u32
+    n_entries, u32 row_off[n_rows + 1], {u16 col, u16 bits}[n] in row-major
+    order of the mask (bf16x_gguf_block.py:131-148)."""
+    b = np.asarray(bits, dtype=np.uint16)
+    rows = b.shape[0]
+    r, c = np.nonzero(ovf_mask_bits(b))
+    row_off = np.zeros(rows + 1, dtype=np.uint32)
+    np.cumsum(np.bincount(r, minlength=rows), out=row_off[1:])
+    ent = np.empty((r.size, 2), dtype=np.uint16)
+    ent[:, 0] = c.astype(np.uint16)
+    ent[:, 1] = b[r, c]
+    return np.array([rows, r.size], dtype=np.uint32).tobytes() + row_off.tobytes() + ent.tobytes()
+
+
+def unpack_ovf(blob: bytes):
+    """-> (n_rows, row_off, cols, bits) (bf16x_gguf_block.py:151-160)."""
+    rows, n = (int(v) for v in np.frombuffer(blob[:OVF_HDR_BYTES], dtype=np.uint32))
+    off = OVF_HDR_BYTES
+    row_off = np.frombuffer(blob[off:off + 4 * (rows + 1)], dtype=np.uint32)
+    off += 4 * (rows + 1)
+    ent = np.frombuffer(blob[off:off + 4 * n], dtype=np.uint16).reshape(-1, 2)
+    return rows, row_off, ent[:, 0], ent[:, 1]
+
+
+def apply_ovf_bits(decoded_bits: np.ndarray, blob: bytes) -> np.ndarray:
+    """Overwrite the table's elements of decoded bits [rows, cols]
+    (bf16x_gguf_block.py:163-171)."""
+    rows, row_off, cols, bits = unpack_ovf(blob)
+    out = np.array(decoded_bits, dtype=np.uint16, copy=True)
+    r = np.repeat(np.arange(rows, dtype=np.int64), np.diff(row_off).astype(np.int64))
+    out[r, cols.astype(np.int64)] = bits
+    return out
+
+
+def dequantize_lossless_bits(packed: np.ndarray, blob: bytes) -> np.ndarray:
+    """blocks + table -> bf16 bits [rows, cols] (bf16x_gguf_block.py:174-178)."""
+    rows = unpack_ovf(blob)[0]
+    dec = dequantize_blocks_bits(packed).reshape(rows, -1)
+    return apply_ovf_bits(dec, blob)
