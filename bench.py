@@ -356,6 +356,21 @@ def main():
     log(f"bf16 F.linear gemv: {sec_bf16 * 1e6:.2f} us ({wd.numel() * 2 / sec_bf16 / 1e9:.1f} GB/s of bf16 bytes)")
     del wcopies
 
+    # ---- device encoder at the headline shape (bf16 weight in HBM -> dict)
+    wdev = w.to(dev)
+    bx.bf16x_quantize(wdev)
+    torch.cuda.synchronize()
+    t_enc = []
+    for _ in range(5):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        bx.bf16x_quantize(wdev)                 # includes the one host read of the table count
+        torch.cuda.synchronize()
+        t_enc.append(time.perf_counter() - t0)
+    enc_rec = {"ms": round(min(t_enc) * 1e3, 3), "GBps_bf16_in": round(wdev.numel() * 2 / min(t_enc) / 1e9, 1)}
+    log(f"device encoder 14336x4096: {enc_rec}")
+    del wdev
+
     # ---- decode (exact) and decode+GEMM at the configuration-3 shape, same rotation
     dec_out = torch.empty(out_f, in_f, dtype=torch.bfloat16, device=dev)
 
@@ -434,6 +449,7 @@ def main():
         "speedup_vs_bf16_gemv": round(sec_bf16 / sec, 3),
         "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 2),
         "decode_exact_14336x4096": decode_rec,
+        "device_encoder_14336x4096": enc_rec,
         "gemm_14336x4096_exact": gemm_rec,
         "gguf_config5": gguf_rec,
         "llama_config4": llama_rec,

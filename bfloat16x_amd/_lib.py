@@ -32,6 +32,9 @@ PROTOTYPES = {
     "bf16x_plan_tiles": (_c_i64, [_c_i64, _c_i64]),
     "bf16x_encode_host": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i32, _P, _P, _P, _P, _P, _P, _c_i64,
                                          ctypes.POINTER(_c_i64), _c_i32]),
+    "bf16x_encode_workspace": (_c_i64, [_c_i64, _c_i64]),
+    "bf16x_encode": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i32, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P,
+                                    _P, _c_i64, _P, _P, _c_i64, _P]),
     "bf16x_plan_host": (ctypes.c_int, [_P, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
                                        _c_i64, _c_i64, _c_i32, _P, _P, _P, _c_i64, ctypes.POINTER(_c_i64)]),
     "bf16x_plan_from_csr": (ctypes.c_int, [_P, _P, _P, _P, _P, _P, _c_i64, _c_i64, _c_i64, _P, _P, _P]),

@@ -34,14 +34,55 @@ def _bf16_bits_host(w: torch.Tensor) -> torch.Tensor:
     return b16.reshape(-1).cpu().contiguous().view(torch.int16)
 
 
+def _quantize_device(w: torch.Tensor) -> dict:
+    """The device encoder (bf16x_encode): outputs on w's GPU."""
+    out_f, in_f = (int(s) for s in w.shape)
+    n = out_f * in_f
+    dev = w.device
+    bits = w.detach().to(torch.bfloat16).contiguous()
+    if bits.data_ptr() % 16:
+        bits = bits.clone()
+    L = _lib.lib()
+    i32 = dict(dtype=torch.int32, device=dev)
+    sign = torch.empty(stream_words(n, 1), **i32)
+    mant = torch.empty(stream_words(n, 7), **i32)
+    delta = torch.empty(stream_words(n, 3), **i32)
+    emax = torch.empty((n + SUB - 1) // SUB, dtype=torch.uint8, device=dev)
+    ws = torch.empty((int(L.bf16x_encode_workspace(out_f, in_f)) + 15) // 16 * 4, **i32)
+    n_ovf = torch.zeros(1, dtype=torch.int64, device=dev)
+    cap = max(1, n // 8)
+    stream = _lib.stream_of(dev)
+    for _ in range(2):
+        idx = torch.empty(cap, **i32)
+        val = torch.empty(cap, dtype=torch.uint8, device=dev)
+        st = L.bf16x_encode(bits.data_ptr(), out_f, in_f, SUB, sign.data_ptr(), sign.numel(), mant.data_ptr(),
+                            mant.numel(), delta.data_ptr(), delta.numel(), emax.data_ptr(), emax.numel(),
+                            idx.data_ptr(), val.data_ptr(), cap, n_ovf.data_ptr(), ws.data_ptr(),
+                            ws.numel() * 4, stream)
+        _lib.check(st, "bf16x_encode")
+        k = int(n_ovf.item())
+        if k <= cap:
+            break
+        cap = k
+    return dict(emax=emax, sign_packed=sign, mant_packed=mant, delta_packed=delta,
+                delta_ovf_idx=idx[:k].clone(), delta_ovf_val=val[:k].clone(),
+                out_f=out_f, in_f=in_f, sub=SUB)
+
+
 def bf16x_quantize(w: torch.Tensor, sub: int = SUB, n_threads: int = 0) -> dict:
-    """bf16 weight [out_f, in_f] -> packed dict of CPU tensors (opqk_linear.py:291).
+    """bf16 weight [out_f, in_f] -> packed dict (opqk_linear.py:291).
 
     Keys: emax (uint8), sign_packed / mant_packed / delta_packed (int32 word
     streams), delta_ovf_idx (int32), delta_ovf_val (uint8), out_f, in_f, sub.
+    A GPU weight is encoded on its GPU (sub = 16) and the dict's tensors stay
+    there, as the reference's torch encoder does on a CUDA tensor; a CPU
+    weight (or another sub) is encoded by the multi-threaded host encoder.
+    Both give the same bytes.
     """
     if w.dim() != 2:
         raise ValueError("bf16x_quantize expects a 2-D weight [out_f, in_f]")
+    if w.is_cuda and int(sub) == SUB and w.numel() <= 2 ** 31 - 1:
+        return _quantize_device(w)
     out_f, in_f = (int(s) for s in w.shape)
     n = out_f * in_f
     bits = _bf16_bits_host(w)

@@ -86,6 +86,20 @@ int bf16x_encode_host(const uint16_t* w_bits, int64_t out_f, int64_t in_f, int32
                       int32_t* ovf_idx, uint8_t* ovf_val, int64_t ovf_cap, int64_t* n_ovf,
                       int32_t n_threads);
 
+/* Device encoder: the same dict as bf16x_encode_host (byte-identical) from a
+ * bf16 weight in device memory, sub = 16 (BF16X_ESUB otherwise).  Replaces
+ * bf16x_quantize on a CUDA tensor (opqk_linear.py:291-324) and the chunked
+ * GPU compressor (compress_bf16x_gpu.py:20-39): no temporaries beyond the
+ * outputs and a workspace of bf16x_encode_workspace bytes (16-byte aligned).
+ * The table count is written to *n_ovf (device int64); entries past ovf_cap
+ * are not written, so a caller whose cap was short re-runs with a larger one.
+ * Streams have at least bf16x_stream_words(N, b) words. */
+int64_t bf16x_encode_workspace(int64_t out_f, int64_t in_f);
+int bf16x_encode(const uint16_t* w_bits, int64_t out_f, int64_t in_f, int32_t sub,
+                 int32_t* sign, int64_t n_sign, int32_t* mant, int64_t n_mant, int32_t* delta, int64_t n_delta,
+                 uint8_t* emax, int64_t n_emax, int32_t* ovf_idx, uint8_t* ovf_val, int64_t ovf_cap,
+                 int64_t* n_ovf, void* workspace, int64_t workspace_bytes, bf16x_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Host plan builder.  Replaces the overflow preparation of Bf16xFused.__init__
  * (bf16x_fused.py:165-182: keep val > 7, per-row CSR) with tile offsets and
