@@ -140,7 +140,12 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // every row on the offsets' latency).  All loads are unconditional (indices
 // clamped): loads under divergent branches make the compiler wait for every
 // outstanding load, which would serialise the prefetch.
-template <int NS, int G, int XT, bool EXACT, bool FULL>
+// EPI = 1 (SwiGLU epilogue, G = 1, iters = 2): the weight's rows come in
+// groups of 8, [gate_4b .. gate_4b+3, up_4b .. up_4b+3], so a wave computes
+// gate_i in its first iteration and up_i in its second and writes
+// y[i] = bf16(bf16(silu(bf16(gate_i))) * bf16(up_i)) (out_f / 2 outputs): the
+// rounding sequence of an unfused GEMV followed by silu(gate) * up in bf16.
+template <int NS, int G, int XT, bool EXACT, bool FULL, int EPI = 0>
 __global__ __launch_bounds__(256) void gemv_pipe_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
     const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
@@ -257,6 +262,7 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
   __syncthreads();
 
   const u32x4* xl = (const u32x4*)lds + (int64_t)(g * NS) * NC * 64 + lane;
+  float gate_keep = 0.f;                                  // EPI = 1: this wave's gate output
   auto body = [&](auto prefetch, int it, Atom* cur, uint32_t* ent, uint8_t* sat, Atom* nxt, uint32_t* entn,
                   uint8_t* satn) {
     constexpr bool PF = decltype(prefetch)::value;
@@ -312,7 +318,15 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
     }
     // reduce and store
     const float tot = wave_sum_dpp(acc0 + acc1);
-    if constexpr (G == 1) {
+    if constexpr (G == 1 && EPI == 1) {
+      const float yb = bf16lo_to_f32(f32_to_bf16_rne(tot));
+      if ((it & 1) == 0) {
+        gate_keep = yb;
+      } else if (lane == 63 && r < out_f) {
+        const float sg = bf16lo_to_f32(f32_to_bf16_rne(gate_keep / (1.0f + __expf(-gate_keep))));
+        y[(r >> 3) * 4 + (r & 3)] = (uint16_t)f32_to_bf16_rne(sg * yb);
+      }
+    } else if constexpr (G == 1) {
       if (lane == 63 && r < out_f) y[r] = (uint16_t)f32_to_bf16_rne(tot);
     } else {
       if (lane == 63) part[it & 1][wave] = tot;
@@ -449,7 +463,52 @@ int launch_gemv(const void* x, const uint32_t* sign, const uint32_t* mant, const
   return launch_status();
 }
 
+// SwiGLU-epilogue GEMV: G = 1 shapes only (in_f <= 4096), iters = 2.
+int launch_gemv_swiglu(const void* x, const uint32_t* sign, const uint32_t* mant, const uint32_t* delta,
+                       const uint16_t* emax2, const uint32_t* to, const uint32_t* te, const uint8_t* ts,
+                       int64_t out_f, int64_t in_f, uint16_t* y, hipStream_t st) {
+  const int64_t P = in_f >> 5;
+  if (out_f % 8 != 0 || P > 128 || tiles_per_row(in_f) != 1 || (out_f + 1) * P * 28 >= (int64_t)0xFFFFFFFF)
+    return BF16X_ESHAPE;
+  const int NS = P > 64 ? 2 : 1;
+  const bool full = P == (int64_t)64 * NS;
+  const size_t lds = (size_t)NS * 64 * 4 * 16;
+  const int64_t grid = out_f / 8;                 // 8 rows = 2 iterations x 4 waves per workgroup
+  if (grid > INT32_MAX) return BF16X_ESHAPE;
+#define BF16X_SW(NS_, EX_, FULL_)                                                                                  \
+  hipLaunchKernelGGL((gemv_pipe_kernel<NS_, 1, BF16X_BF16, EX_, FULL_, 1>), dim3((unsigned)grid), dim3(256), lds, \
+                     st, x, sign, mant, delta, emax2, to, te, ts, out_f, in_f, 2, y)
+  if (NS == 2) {
+    if (to) { if (full) BF16X_SW(2, true, true); else BF16X_SW(2, true, false); }
+    else { if (full) BF16X_SW(2, false, true); else BF16X_SW(2, false, false); }
+  } else {
+    if (to) { if (full) BF16X_SW(1, true, true); else BF16X_SW(1, true, false); }
+    else { if (full) BF16X_SW(1, false, true); else BF16X_SW(1, false, false); }
+  }
+#undef BF16X_SW
+  return launch_status();
+}
+
 }  // namespace
+
+extern "C" int bf16x_gemv_swiglu(const void* x, const int32_t* sign, int64_t n_sign, const int32_t* mant,
+                                 int64_t n_mant, const int32_t* delta, int64_t n_delta, const uint8_t* emax,
+                                 int64_t n_emax, const uint32_t* tile_off, const uint32_t* tile_ent,
+                                 const uint8_t* tile_sat, int64_t out_f, int64_t in_f, int32_t mode, uint16_t* y,
+                                 bf16x_stream_t stream) {
+  if (!x || !sign || !mant || !delta || !emax || !y) return BF16X_EARG;
+  if (mode != BF16X_EXACT && mode != BF16X_SATURATED) return BF16X_EARG;
+  int rc = check_dict(out_f, in_f, 16, n_sign, n_mant, n_delta, n_emax);
+  if (rc) return rc;
+  if (in_f % 32 != 0) return BF16X_ESHAPE;
+  if (mode == BF16X_EXACT && (!tile_off || !tile_ent || !tile_sat)) return BF16X_EARG;
+  if (!aligned4(x) || !aligned4(sign) || !aligned4(mant) || !aligned4(delta) || !aligned2(emax) || !aligned2(y))
+    return BF16X_EARG;
+  const bool ex = mode == BF16X_EXACT;
+  return launch_gemv_swiglu(x, (const uint32_t*)sign, (const uint32_t*)mant, (const uint32_t*)delta,
+                            (const uint16_t*)emax, ex ? tile_off : nullptr, ex ? tile_ent : nullptr,
+                            ex ? tile_sat : nullptr, out_f, in_f, y, (hipStream_t)stream);
+}
 
 extern "C" int bf16x_gemv(const void* x, int32_t x_dtype, const int32_t* sign, int64_t n_sign,
                           const int32_t* mant, int64_t n_mant, const int32_t* delta, int64_t n_delta,

@@ -494,14 +494,25 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t* __rest
 
 // ---------------------------------------------------------------------------
 // SwiGLU over 8 columns per thread.
+// PAIRS8: a 16-byte chunk of 8 gate_up columns holds gate 4b .. 4b+3 and
+// up 4b .. 4b+3; two chunks give 8 outputs.
+template <bool PAIRS8>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, int64_t T, int F,
                                                        uint16_t* __restrict__ out) {
   const int64_t chunks = T * (F / 8);
   for (int64_t id = (int64_t)blockIdx.x * 256 + threadIdx.x; id < chunks; id += (int64_t)gridDim.x * 256) {
     const int64_t t = id / (F / 8);
     const int c = (int)(id - t * (F / 8)) * 8;
-    const u32x4 gv = *(const u32x4*)(gu + t * 2 * F + c);
-    const u32x4 uv = *(const u32x4*)(gu + t * 2 * F + F + c);
+    u32x4 gv, uv;
+    if constexpr (PAIRS8) {
+      const u32x4 a = *(const u32x4*)(gu + t * 2 * F + 2 * c);       // gate c..c+3, up c..c+3
+      const u32x4 b = *(const u32x4*)(gu + t * 2 * F + 2 * c + 8);   // gate c+4..c+7, up c+4..c+7
+      gv = u32x4{a.x, a.y, b.x, b.y};
+      uv = u32x4{a.z, a.w, b.z, b.w};
+    } else {
+      gv = *(const u32x4*)(gu + t * 2 * F + c);
+      uv = *(const u32x4*)(gu + t * 2 * F + F + c);
+    }
     const uint32_t g[4] = {gv.x, gv.y, gv.z, gv.w}, u[4] = {uv.x, uv.y, uv.z, uv.w};
     uint32_t o[4];
 #pragma unroll
@@ -666,16 +677,20 @@ extern "C" int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, c
   return launch_status();
 }
 
-extern "C" int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t ffn, uint16_t* out,
+extern "C" int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t ffn, int32_t layout, uint16_t* out,
                               bf16x_stream_t stream) {
-  if (!gate_up || !out || tokens < 0) return BF16X_EARG;
+  if (!gate_up || !out || tokens < 0 || (layout != BF16X_SPLIT && layout != BF16X_PAIRS8)) return BF16X_EARG;
   if (ffn <= 0 || ffn % 8 != 0 || ffn > INT32_MAX / 2) return BF16X_ESHAPE;
   if (!aligned16(gate_up) || !aligned16(out)) return BF16X_EARG;
   if (tokens == 0) return BF16X_OK;
   const int64_t chunks = tokens * (ffn / 8);
   const int64_t grid = std::min<int64_t>((chunks + 255) / 256, 8192);
-  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, gate_up, tokens,
-                     (int)ffn, out);
+  if (layout == BF16X_PAIRS8)
+    hipLaunchKernelGGL(silu_mul_kernel<true>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, gate_up,
+                       tokens, (int)ffn, out);
+  else
+    hipLaunchKernelGGL(silu_mul_kernel<false>, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, gate_up,
+                       tokens, (int)ffn, out);
   return launch_status();
 }
 

@@ -15,9 +15,11 @@ device-resident state:
   * the ops between the linears are the kernels of include/bf16x_llama.h:
     per layer RMSNorm(+residual), qkv GEMV, RoPE + KV append + attention
     (one launch per token), o GEMV, RMSNorm(+residual), gate_up GEMV,
-    SwiGLU, down GEMV: 8 launches;
-  * q/k/v and gate/up are single fused linears ([q; k; v] and [gate; up]
-    rows), so batch-1 decode runs 4 GEMVs per layer.
+    SwiGLU, down GEMV;
+  * q/k/v and gate/up are single fused linears, so batch-1 decode runs 4
+    GEMVs per layer; gate_up's rows are stored in groups of 8 [gate 4b ..
+    4b+3, up 4b .. 4b+3] (pairs8_rows) so that the BF16X gate_up GEMV applies
+    SwiGLU in its epilogue (bf16x_gemv_swiglu): decode runs 7 launches per layer.
 
 Shapes of the benchmark configuration (the defaults of LlamaConfig): 32
 layers, hidden 4096, FFN 14336 (SwiGLU), 32 query / 8 KV heads, head_dim 128,
@@ -33,9 +35,9 @@ import math
 import torch
 from torch import nn
 
-from . import _lib
+from . import _lib, ops
 
-__all__ = ["LlamaConfig", "LlamaStack", "LlamaRunner", "rope_table", "rmsnorm", "rope_kv", "attention",
+__all__ = ["LlamaConfig", "LlamaStack", "LlamaRunner", "rope_table", "rmsnorm", "rope_kv", "attention", "pairs8_rows",
            "attention_decode", "attention_decode_supported", "attention_decode_workspace", "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
 
 NORM_ADD, NORM_STORE = 1, 2
@@ -191,14 +193,24 @@ def attention_decode(qkv, pos, cos_sin, n_heads, n_kv_heads, k_cache, v_cache, o
     _lib.check(st, "bf16x_attention_decode")
 
 
-def silu_mul(gate_up, out, ffn):
-    """out[t] = silu(gate_up[t, :ffn]) * gate_up[t, ffn:]."""
+def pairs8_rows(ffn: int) -> torch.Tensor:
+    """Natural row of each row of a PAIRS8 gate_up weight: groups of 8 rows
+    [gate 4b .. 4b+3, up 4b .. 4b+3] from the natural [gate; up] order."""
+    b = torch.arange(ffn // 4).repeat_interleave(8) * 4
+    k = torch.arange(8).repeat(ffn // 4)
+    return torch.where(k < 4, b + k, ffn + b + k - 4)
+
+
+def silu_mul(gate_up, out, ffn, pairs8=False):
+    """out[t] = silu(gate) * up of gate_up row t: natural [gate | up] columns,
+    or (pairs8) groups of 8 [gate 4b .. 4b+3 | up 4b .. 4b+3]."""
     _bf16_dev(gate_up, "gate_up")
     _bf16_dev(out, "out")
     _need(gate_up.numel() % (2 * ffn) == 0, "gate_up is not a whole number of tokens")
     tokens = gate_up.numel() // (2 * ffn)
     _need(out.numel() >= tokens * ffn, "out too small")
-    st = _lib.lib().bf16x_silu_mul(gate_up.data_ptr(), tokens, ffn, out.data_ptr(), _stream(gate_up))
+    st = _lib.lib().bf16x_silu_mul(gate_up.data_ptr(), tokens, ffn, 1 if pairs8 else 0, out.data_ptr(),
+                                   _stream(gate_up))
     _lib.check(st, "bf16x_silu_mul")
 
 
@@ -224,6 +236,13 @@ def rope_table(max_len: int, theta: float, device) -> torch.Tensor:
 
 # ---------------------------------------------------------------------------
 # the model
+
+def _swiglu_gemv_ok(mod) -> bool:
+    """A deployed BF16X gate_up the SwiGLU-epilogue GEMV can run."""
+    from .nn import Bf16xFused
+    return (isinstance(mod, Bf16xFused) and mod.mode == "fused" and mod._bias is None
+            and mod.in_features <= 4096 and mod.out_features % 8 == 0)
+
 
 def _device(device):
     if device is None:
@@ -257,12 +276,16 @@ class LlamaStack(nn.Module):
         ones = lambda: nn.Parameter(torch.ones(cfg.hidden, dtype=torch.bfloat16, device=dev), requires_grad=False)
         self.embed = nn.Parameter(rnd((cfg.vocab, cfg.hidden), 1), requires_grad=False)
         self.layers = nn.ModuleList()
+        perm = pairs8_rows(cfg.ffn).to(dev)
         for i in range(cfg.n_layers):
             lay = nn.Module()
             lay.attn_norm = ones()
             lay.mlp_norm = ones()
             for j, (name, o, n) in enumerate(cfg.linear_shapes()):
-                setattr(lay, name, _linear(rnd((o, n), 16 + 8 * i + j)))
+                w = rnd((o, n), 16 + 8 * i + j)
+                if name == "gate_up":             # rows in PAIRS8 order (pairs8_rows)
+                    w = w[perm].contiguous()
+                setattr(lay, name, _linear(w))
             self.layers.append(lay)
         self.norm = ones()
         self.lm_head = _linear(rnd((cfg.vocab, cfg.hidden), 2))
@@ -338,8 +361,13 @@ class LlamaRunner:
                 attention(self.q, self.k_cache[i], self.v_cache[i], pos, H, KV, self.attn, tokens=T)
             o = lay.o(rows(self.attn))
             rmsnorm(o, lay.mlp_norm, self.normed, self.residual, flags=NORM_ADD | NORM_STORE, eps=cfg.eps)
-            gu = lay.gate_up(rows(self.normed))
-            silu_mul(gu, self.act, cfg.ffn)
+            gu_mod = lay.gate_up
+            if one and _swiglu_gemv_ok(gu_mod):
+                # fused decode+GEMV with the SwiGLU epilogue: no gate_up round trip, one launch
+                ops.bf16x_gemv_swiglu(self.normed[0], gu_mod._sign, gu_mod._mant, gu_mod._delta, gu_mod._emax,
+                                      gu_mod.out_features, gu_mod.in_features, plan=gu_mod._plan, out=self.act[0])
+            else:
+                silu_mul(gu_mod(rows(self.normed)), self.act, cfg.ffn, pairs8=True)
             prev = lay.down(rows(self.act))
         return prev
 

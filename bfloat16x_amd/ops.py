@@ -138,6 +138,29 @@ def bf16x_gemv(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None =
     return y
 
 
+def bf16x_gemv_swiglu(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None = None,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """act[out_f // 2] (bf16) = silu(gate) * up of the GEMV W . x, W's rows in
+    groups of 8 [gate 4b .. 4b+3, up 4b .. 4b+3] (include/bf16x_llama.h)."""
+    s, m, d, e = _streams(sign, mant, delta, emax)
+    xx = _dev_tensor(x, "x", (torch.bfloat16,)).reshape(-1)
+    out_f, in_f = int(out_f), int(in_f)
+    if xx.numel() != in_f:
+        raise ValueError(f"x has {xx.numel()} elements, in_f = {in_f}")
+    y = out if out is not None else torch.empty(out_f // 2, dtype=torch.bfloat16, device=s.device)
+    if y.dtype != torch.bfloat16 or not y.is_contiguous() or y.numel() < out_f // 2:
+        raise ValueError("out must be a contiguous bf16 tensor of out_f / 2 elements")
+    mode = _lib.SATURATED if plan is None else _lib.EXACT
+    st = _lib.lib().bf16x_gemv_swiglu(xx.data_ptr(), s.data_ptr(), s.numel(), m.data_ptr(), m.numel(), d.data_ptr(),
+                                      d.numel(), e.data_ptr(), e.numel(),
+                                      _lib.ptr(plan.tile_off) if plan else None,
+                                      _lib.ptr(plan.tile_ent) if plan else None,
+                                      _lib.ptr(plan.tile_sat) if plan else None, out_f, in_f, mode, y.data_ptr(),
+                                      _lib.stream_of(s.device))
+    _lib.check(st, "bf16x_gemv_swiglu")
+    return y
+
+
 def bf16x_fused_gemv(x, sign, mant, delta, emax, olk, old, oloff, out_f, in_f, group=16, r=4, bk=256,
                      num_warps=2, *, plan: Bf16xPlan | None = None) -> torch.Tensor:
     """Fused decode+GEMV with the reference's signature (bf16x_fused.py:114).

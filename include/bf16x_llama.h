@@ -83,9 +83,26 @@ int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, const float*
                            uint16_t* k_cache, uint16_t* v_cache, void* workspace, int64_t workspace_bytes,
                            uint16_t* out, bf16x_stream_t stream);
 
-/* SwiGLU: out[t][i] = bf16(bf16(silu(gate[t][i])) * up[t][i]).  ffn % 8 == 0,
- * 16-byte aligned buffers. */
-int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t ffn, uint16_t* out, bf16x_stream_t stream);
+/* SwiGLU: out[t][i] = bf16(bf16(silu(gate_i)) * up_i) of the gate_up row t.
+ * layout 0: gate columns 0 .. ffn-1, then up columns (gate_i at i, up_i at
+ * ffn + i); layout 1 (BF16X_PAIRS8): groups of 8 columns [gate 4b .. 4b+3,
+ * up 4b .. 4b+3] (gate_i at 8(i/4) + i%4, up_i at 8(i/4) + 4 + i%4), the row
+ * order bf16x_gemv_swiglu consumes.  ffn % 8 == 0, 16-byte aligned buffers. */
+enum { BF16X_SPLIT = 0, BF16X_PAIRS8 = 1 };
+int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t ffn, int32_t layout, uint16_t* out,
+                   bf16x_stream_t stream);
+
+/* Fused decode+GEMV with the SwiGLU epilogue: a packed dict [2 ffn, in_f]
+ * whose rows are in the BF16X_PAIRS8 order gives out[i] = bf16(bf16(silu(
+ * bf16(W x)_gate_i)) * bf16(W x)_up_i), i < ffn, with the rounding of
+ * bf16x_gemv followed by bf16x_silu_mul.  x bf16 (4-byte aligned), 2 ffn % 8
+ * == 0, in_f <= 4096 (one wave per row); arguments otherwise as bf16x_gemv
+ * (sub 16).  Replaces the gate/up projections and the activation of the
+ * reference harness's MLP (three modules of the Hugging Face model). */
+int bf16x_gemv_swiglu(const void* x, const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                      const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                      const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
+                      int64_t in_f, int32_t mode, uint16_t* out, bf16x_stream_t stream);
 
 /* Greedy step: token[0] = argmax(logits[0 .. vocab)) (the first maximum),
  * history[state[1]] = token[0] when state[1] < history_len, then state[1]++

@@ -13,6 +13,7 @@ import pytest
 import torch
 
 from bfloat16x_amd import llama
+from oracle import dict_codec as dc
 from tests.test_gpu_dict import DEV
 
 pytestmark = pytest.mark.gpu
@@ -187,14 +188,44 @@ def test_attention_decode_matches_two_launch_path(bx, H, KV, pos, L):
 
 
 @torch.no_grad()
-def test_silu_mul(bx):
+@pytest.mark.parametrize("pairs8", [False, True])
+def test_silu_mul(bx, pairs8):
     T, F = 3, 1536
     gu = rnd((T, 2 * F), 11, 3.0)
     out = torch.empty(T, F, dtype=torch.bfloat16, device=DEV)
-    llama.silu_mul(gu.to(DEV), out, F)
+    src = gu[:, llama.pairs8_rows(F)].contiguous() if pairs8 else gu
+    llama.silu_mul(src.to(DEV), out, F, pairs8=pairs8)
     g, u = gu[:, :F].float(), gu[:, F:].float()
     ref = bf(bf(g * torch.sigmoid(g)) * u)
     within_ulps(out, ref, 1.0)
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("F,in_f,mode", [(1536, 512, "exact"), (14336, 4096, "exact"), (1024, 2048, "saturated"),
+                                         (256, 64, "exact")])
+def test_gemv_swiglu_matches_unfused(bx, F, in_f, mode):
+    """The SwiGLU-epilogue GEMV equals the plain GEMV followed by silu_mul
+    (bit for bit: same sums, same roundings) and the fp64 product."""
+    from bfloat16x_amd import ops
+    bits = dc.bench_weight_bits(2 * F, in_f, seed=12)
+    w = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+    wp = w[llama.pairs8_rows(F)].contiguous()
+    d = bx.bf16x_quantize(wp.to(DEV))
+    plan = bx.build_plan_host(d, device=DEV) if mode == "exact" else None
+    x = rnd(in_f, 13).to(DEV)
+    args = (d["sign_packed"], d["mant_packed"], d["delta_packed"], d["emax"], 2 * F, in_f)
+    act = ops.bf16x_gemv_swiglu(x, *args, plan=plan)
+    y = ops.bf16x_gemv(x, *args, plan=plan)
+    ref = torch.empty(F, dtype=torch.bfloat16, device=DEV)
+    llama.silu_mul(y, ref, F, pairs8=True)
+    assert torch.equal(act, ref)
+    if mode == "exact":
+        # fp64 product through the same bf16 rounding chain (gate, up, silu,
+        # product): within 3 ulps (the fp32 sums may round gate/up the other way)
+        yw = torch.from_numpy(w.double().numpy() @ x.double().cpu().numpy())
+        g, u = bf(yw[:F].float()), bf(yw[F:].float())
+        ref64 = bf(bf(g * torch.sigmoid(g)) * u)
+        within_ulps(act, ref64, 3.0, floor=1e-3 * float(ref64.abs().mean()))
 
 
 @torch.no_grad()
@@ -241,10 +272,18 @@ def ref_forward(W, cfg, ids):
 
 
 def host_weights(model):
+    """fp32 CPU weights, gate_up back in the natural [gate; up] row order."""
     f = lambda t: t.detach().float().cpu()
-    return {"embed": f(model.embed), "norm": f(model.norm), "lm_head": f(model.lm_head.weight),
-            "layers": [{k: f(getattr(l, k).weight if k in ("qkv", "o", "gate_up", "down") else getattr(l, k))
-                        for k in ("attn_norm", "mlp_norm", "qkv", "o", "gate_up", "down")} for l in model.layers]}
+    perm = llama.pairs8_rows(model.cfg.ffn)
+    layers = []
+    for l in model.layers:
+        lw = {k: f(getattr(l, k).weight if k in ("qkv", "o", "gate_up", "down") else getattr(l, k))
+              for k in ("attn_norm", "mlp_norm", "qkv", "o", "gate_up", "down")}
+        nat = torch.empty_like(lw["gate_up"])
+        nat[perm] = lw["gate_up"]
+        lw["gate_up"] = nat
+        layers.append(lw)
+    return {"embed": f(model.embed), "norm": f(model.norm), "lm_head": f(model.lm_head.weight), "layers": layers}
 
 
 @pytest.fixture(scope="module")

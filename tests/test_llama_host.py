@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from bfloat16x_amd import _lib, llama
+from bfloat16x_amd.codec import stream_words
 
 
 def test_config_defaults_are_the_benchmark_stack():
@@ -65,15 +66,29 @@ def test_entry_points_validate_before_launch():
     assert _call("bf16x_attention_decode_workspace", 32, 8, 640) > 0
     assert _call("bf16x_attention_decode", p, p, p, 24, 8, 128, 640, 0.1, p, p, p, 1 << 20, p, None) == _lib.ESHAPE
     assert _call("bf16x_attention_decode", p, p, p, 32, 8, 128, 640, 0.1, p, p, p, 64, p, None) == _lib.ECAPACITY
-    # silu_mul: ffn % 8
-    assert _call("bf16x_silu_mul", p, 1, 12, p, None) == _lib.ESHAPE
+    # silu_mul: ffn % 8, layout code
+    assert _call("bf16x_silu_mul", p, 1, 12, 0, p, None) == _lib.ESHAPE
+    assert _call("bf16x_silu_mul", p, 1, 16, 2, p, None) == _lib.EARG
+    # SwiGLU GEMV: out_f % 8, in_f beyond one wave per row, mode
+    def lens(o, i):
+        n = o * i
+        return stream_words(n, 1), stream_words(n, 7), stream_words(n, 3), (n + 15) // 16
+
+    ls_, lm_, ld_, le_ = lens(12, 2048)
+    assert _call("bf16x_gemv_swiglu", p, p, ls_, p, lm_, p, ld_, p, le_, p, p, p, 12, 2048, 1, p, None) == \
+        _lib.ESHAPE                                                       # out_f % 8
+    ls_, lm_, ld_, le_ = lens(16, 8192)
+    assert _call("bf16x_gemv_swiglu", p, p, ls_, p, lm_, p, ld_, p, le_, p, p, p, 16, 8192, 1, p, None) == \
+        _lib.ESHAPE                                                       # in_f > 4096
+    ls_, lm_, ld_, le_ = lens(16, 128)
+    assert _call("bf16x_gemv_swiglu", p, p, ls_, p, lm_, p, ld_, p, le_, p, p, p, 16, 128, 5, p, None) == _lib.EARG
     # greedy: misaligned token, history without length
     assert _call("bf16x_greedy", p, 8, p + 4, p, p, 1, None) == _lib.EARG
     assert _call("bf16x_greedy", p, 8, p, p, None, 1, None) == _lib.EARG
     assert _call("bf16x_greedy", p, 0, p, p, p, 1, None) == _lib.ESHAPE
     # zero rows / tokens: nothing to launch
     assert _call("bf16x_rmsnorm", p, None, 0, None, p, p, 0, 64, 1e-5, 0, None) == _lib.OK
-    assert _call("bf16x_silu_mul", p, 0, 16, p, None) == _lib.OK
+    assert _call("bf16x_silu_mul", p, 0, 16, 1, p, None) == _lib.OK
 
 
 def test_wrappers_refuse_cpu_tensors():
@@ -84,3 +99,11 @@ def test_wrappers_refuse_cpu_tensors():
         llama.silu_mul(torch.zeros(2, 32, dtype=torch.bfloat16), torch.zeros(2, 16, dtype=torch.bfloat16), 16)
     with pytest.raises(RuntimeError):
         llama.LlamaStack(llama.LlamaConfig(n_layers=1, hidden=512, ffn=1024, n_heads=4, n_kv_heads=2, vocab=64))
+
+
+def test_pairs8_rows_is_the_grouped_permutation():
+    perm = llama.pairs8_rows(16)
+    assert perm.tolist() == [0, 1, 2, 3, 16, 17, 18, 19, 4, 5, 6, 7, 20, 21, 22, 23,
+                             8, 9, 10, 11, 24, 25, 26, 27, 12, 13, 14, 15, 28, 29, 30, 31]
+    big = llama.pairs8_rows(14336)
+    assert torch.equal(torch.sort(big).values, torch.arange(2 * 14336))
