@@ -67,6 +67,8 @@ PROTOTYPES = {
     "bf16x_attention_decode": (ctypes.c_int, [_P, _P, _P, _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _P, _P,
                                               _P, _c_i64, _P, _P]),
     "bf16x_silu_mul": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i32, _P, _P]),
+    "bf16x_gemv_norm": (ctypes.c_int, [_P, _P, _P, _P, ctypes.c_float, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P,
+                                       _c_i64, _P, _P, _P, _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
     "bf16x_gemv_swiglu": (ctypes.c_int, [_P, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P, _P, _c_i64,
                                          _c_i64, _c_i32, _P, _P]),
     "bf16x_greedy": (ctypes.c_int, [_P, _c_i64, _P, _P, _P, _c_i64, _P]),

@@ -145,12 +145,27 @@ __device__ __forceinline__ float wave_sum_dpp(float v) {
 // gate_i in its first iteration and up_i in its second and writes
 // y[i] = bf16(bf16(silu(bf16(gate_i))) * bf16(up_i)) (out_f / 2 outputs): the
 // rounding sequence of an unfused GEMV followed by silu(gate) * up in bf16.
-template <int NS, int G, int XT, bool EXACT, bool FULL, int EPI = 0>
+//
+// XM = 1 (RMSNorm staging, bf16 x): the x the rows are multiplied with is
+// RMSNorm(h) * w with h = bf16(x + res_in) (or x when res_in is null),
+// computed by every workgroup from x, res_in and w while it stages x, with
+// the roundings of the standalone RMSNorm kernel (bf16(bf16(h * rsqrt(mean
+// (h^2) + eps)) * w)); workgroup 0 also stores h to res_out (a buffer no
+// workgroup of this launch reads).
+struct NormArgs {
+  const uint16_t* res_in;
+  const uint16_t* w;
+  uint16_t* res_out;
+  float eps;
+};
+
+template <int NS, int G, int XT, bool EXACT, bool FULL, int EPI = 0, int XM = 0>
 __global__ __launch_bounds__(256) void gemv_pipe_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
     const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
     const uint32_t* __restrict__ tile_off, const uint32_t* __restrict__ tile_ent,
-    const uint8_t* __restrict__ tile_sat, int64_t out_f, int64_t in_f, int iters, uint16_t* __restrict__ y) {
+    const uint8_t* __restrict__ tile_sat, int64_t out_f, int64_t in_f, int iters, uint16_t* __restrict__ y,
+    NormArgs na = NormArgs{nullptr, nullptr, nullptr, 0.f}) {
   constexpr int RPI = 4 / G;                              // rows per workgroup iteration
   constexpr int XW = (XT == BF16X_BF16) ? 16 : 32;        // x words per atom
   constexpr int NC = XW / 4;                              // 16-byte chunks per atom
@@ -242,12 +257,77 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
   }
   constexpr int XSLOTS = (G * APW + 255) / 256;  // x atoms staged per thread (<= 2)
   uint32_t xs_reg[XSLOTS][XW];
+  [[maybe_unused]] uint32_t wn_reg[XM == 1 ? XSLOTS : 1][XM == 1 ? XW : 1];
+  [[maybe_unused]] float ssq = 0.f;
 #pragma unroll
   for (int i = 0; i < XSLOTS; ++i) {
     const int slot = threadIdx.x + 256 * i;
-    load_x_atom<XT>(x, min((int64_t)slot, P - 1), xs_reg[i]);  // slot index = atom index
+    if constexpr (XM == 1) {
+      static_assert(XT == BF16X_BF16, "the RMSNorm staging takes bf16 x");
+      const int64_t a = min((int64_t)slot, P - 1);
+      const uint16_t* xa = (const uint16_t*)x + 32 * a;
+      uint32_t hw[16];                                     // h, natural order, bf16 pairs
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4a xv = *(const u32x4a*)(xa + 8 * c);
+        u32x4a rv = u32x4a{0u, 0u, 0u, 0u};
+        if (na.res_in) rv = *(const u32x4a*)(na.res_in + 32 * a + 8 * c);
+        const uint32_t xw4[4] = {xv.x, xv.y, xv.z, xv.w}, rw4[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          uint32_t lo = xw4[k] & 0xFFFFu, hi = xw4[k] >> 16;
+          if (na.res_in) {
+            lo = f32_to_bf16_rne(bf16lo_to_f32(xw4[k]) + bf16lo_to_f32(rw4[k]));
+            hi = f32_to_bf16_rne(bf16hi_to_f32(xw4[k]) + bf16hi_to_f32(rw4[k]));
+          }
+          hw[4 * c + k] = lo | (hi << 16);
+        }
+      }
+      load_x_atom<XT>(na.w, a, wn_reg[i]);
+      if (slot < P) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          const float lo = bf16lo_to_f32(hw[k]), hi = bf16hi_to_f32(hw[k]);
+          ssq += lo * lo + hi * hi;
+        }
+        if (blockIdx.x == 0 && na.res_out) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            *(u32x4a*)(na.res_out + 32 * a + 8 * c) = u32x4a{hw[4 * c], hw[4 * c + 1], hw[4 * c + 2], hw[4 * c + 3]};
+        }
+      }
+      // natural -> pair order (element j, j + 16), as load_x_atom
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        xs_reg[i][2 * k] = perm(hw[8 + k], hw[k], 0x05040100u);
+        xs_reg[i][2 * k + 1] = perm(hw[8 + k], hw[k], 0x07060302u);
+      }
+    } else {
+      load_x_atom<XT>(x, min((int64_t)slot, P - 1), xs_reg[i]);  // slot index = atom index
+    }
   }
   load_row(r, bufA);
+  // the first row's entries go out before the staging waits (XM = 1 waits for
+  // its loads and a barrier before the x stores)
+  if constexpr (EXACT && XM == 1) load_ents(eb, ee, entA, satA);
+  if constexpr (XM == 1) {
+    // sum of squares over the row, then x = bf16(bf16(h * s) * w) in place
+    __shared__ float nred[4];
+    float v = wave_sum_dpp(ssq);
+    if (lane == 63) nred[wave] = v;
+    __syncthreads();
+    const float tot = (nred[0] + nred[1]) + (nred[2] + nred[3]);
+    const float sc = 1.0f / sqrtf(tot / (float)in_f + na.eps);
+#pragma unroll
+    for (int i = 0; i < XSLOTS; ++i)
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const uint32_t h = xs_reg[i][k], w = wn_reg[i][k];
+        const float lo = bf16lo_to_f32(f32_to_bf16_rne(bf16lo_to_f32(h) * sc)) * bf16lo_to_f32(w);
+        const float hi = bf16lo_to_f32(f32_to_bf16_rne(bf16hi_to_f32(h) * sc)) * bf16hi_to_f32(w);
+        xs_reg[i][k] = f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+      }
+  }
 #pragma unroll
   for (int i = 0; i < XSLOTS; ++i) {
     const int slot = threadIdx.x + 256 * i;
@@ -258,7 +338,7 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
         dst[c * 64] = u32x4{xs_reg[i][4 * c], xs_reg[i][4 * c + 1], xs_reg[i][4 * c + 2], xs_reg[i][4 * c + 3]};
     }
   }
-  if constexpr (EXACT) load_ents(eb, ee, entA, satA);
+  if constexpr (EXACT && XM == 0) load_ents(eb, ee, entA, satA);
   __syncthreads();
 
   const u32x4* xl = (const u32x4*)lds + (int64_t)(g * NS) * NC * 64 + lane;
@@ -463,30 +543,58 @@ int launch_gemv(const void* x, const uint32_t* sign, const uint32_t* mant, const
   return launch_status();
 }
 
-// SwiGLU-epilogue GEMV: G = 1 shapes only (in_f <= 4096), iters = 2.
-int launch_gemv_swiglu(const void* x, const uint32_t* sign, const uint32_t* mant, const uint32_t* delta,
-                       const uint16_t* emax2, const uint32_t* to, const uint32_t* te, const uint8_t* ts,
-                       int64_t out_f, int64_t in_f, uint16_t* y, hipStream_t st) {
+// One-wave-per-row GEMV variants (G = 1, in_f <= 4096): EPI = 1 SwiGLU
+// epilogue (iters = 2), XM = 1 RMSNorm staging.
+template <int EPI, int XM>
+int launch_gemv_g1(const void* x, const uint32_t* sign, const uint32_t* mant, const uint32_t* delta,
+                   const uint16_t* emax2, const uint32_t* to, const uint32_t* te, const uint8_t* ts, int64_t out_f,
+                   int64_t in_f, uint16_t* y, NormArgs na, hipStream_t st) {
   const int64_t P = in_f >> 5;
-  if (out_f % 8 != 0 || P > 128 || tiles_per_row(in_f) != 1 || (out_f + 1) * P * 28 >= (int64_t)0xFFFFFFFF)
+  if ((EPI == 1 && out_f % 8 != 0) || P > 128 || tiles_per_row(in_f) != 1 ||
+      (out_f + 1) * P * 28 >= (int64_t)0xFFFFFFFF)
     return BF16X_ESHAPE;
   const int NS = P > 64 ? 2 : 1;
   const bool full = P == (int64_t)64 * NS;
   const size_t lds = (size_t)NS * 64 * 4 * 16;
-  const int64_t grid = out_f / 8;                 // 8 rows = 2 iterations x 4 waves per workgroup
-  if (grid > INT32_MAX) return BF16X_ESHAPE;
-#define BF16X_SW(NS_, EX_, FULL_)                                                                                  \
-  hipLaunchKernelGGL((gemv_pipe_kernel<NS_, 1, BF16X_BF16, EX_, FULL_, 1>), dim3((unsigned)grid), dim3(256), lds, \
-                     st, x, sign, mant, delta, emax2, to, te, ts, out_f, in_f, 2, y)
-  if (NS == 2) {
-    if (to) { if (full) BF16X_SW(2, true, true); else BF16X_SW(2, true, false); }
-    else { if (full) BF16X_SW(2, false, true); else BF16X_SW(2, false, false); }
-  } else {
-    if (to) { if (full) BF16X_SW(1, true, true); else BF16X_SW(1, true, false); }
-    else { if (full) BF16X_SW(1, false, true); else BF16X_SW(1, false, false); }
+  const int64_t groups = (out_f + 3) / 4;
+  int iters = EPI == 1 ? 2 : (groups >= 2048 ? 2 : 1);
+  if (XM == 1) {
+    // every workgroup normalises x in its prologue: enough rows per
+    // workgroup that the grid fits one round of resident workgroups (4 per CU)
+    const int64_t slots = 1024;
+    iters = std::max<int64_t>(iters, (groups + slots - 1) / slots);
+    if (EPI == 1) iters += iters & 1;
   }
-#undef BF16X_SW
+  // EPI = 1: an even iters starts every workgroup on a row group of 8 (out_f % 8 == 0)
+  const int64_t grid = (groups + iters - 1) / iters;
+  if (grid > INT32_MAX) return BF16X_ESHAPE;
+#define BF16X_G1(NS_, EX_, FULL_)                                                                                \
+  hipLaunchKernelGGL((gemv_pipe_kernel<NS_, 1, BF16X_BF16, EX_, FULL_, EPI, XM>), dim3((unsigned)grid), dim3(256), \
+                     lds, st, x, sign, mant, delta, emax2, to, te, ts, out_f, in_f, iters, y, na)
+  if (NS == 2) {
+    if (to) { if (full) BF16X_G1(2, true, true); else BF16X_G1(2, true, false); }
+    else { if (full) BF16X_G1(2, false, true); else BF16X_G1(2, false, false); }
+  } else {
+    if (to) { if (full) BF16X_G1(1, true, true); else BF16X_G1(1, true, false); }
+    else { if (full) BF16X_G1(1, false, true); else BF16X_G1(1, false, false); }
+  }
+#undef BF16X_G1
   return launch_status();
+}
+
+int check_gemv_args(const void* x, const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                    const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                    const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
+                    int64_t in_f, int32_t mode, const uint16_t* y) {
+  if (!x || !sign || !mant || !delta || !emax || !y) return BF16X_EARG;
+  if (mode != BF16X_EXACT && mode != BF16X_SATURATED) return BF16X_EARG;
+  const int rc = check_dict(out_f, in_f, 16, n_sign, n_mant, n_delta, n_emax);
+  if (rc) return rc;
+  if (in_f % 32 != 0) return BF16X_ESHAPE;
+  if (mode == BF16X_EXACT && (!tile_off || !tile_ent || !tile_sat)) return BF16X_EARG;
+  if (!aligned4(x) || !aligned4(sign) || !aligned4(mant) || !aligned4(delta) || !aligned2(emax) || !aligned2(y))
+    return BF16X_EARG;
+  return BF16X_OK;
 }
 
 }  // namespace
@@ -496,18 +604,38 @@ extern "C" int bf16x_gemv_swiglu(const void* x, const int32_t* sign, int64_t n_s
                                  int64_t n_emax, const uint32_t* tile_off, const uint32_t* tile_ent,
                                  const uint8_t* tile_sat, int64_t out_f, int64_t in_f, int32_t mode, uint16_t* y,
                                  bf16x_stream_t stream) {
-  if (!x || !sign || !mant || !delta || !emax || !y) return BF16X_EARG;
-  if (mode != BF16X_EXACT && mode != BF16X_SATURATED) return BF16X_EARG;
-  int rc = check_dict(out_f, in_f, 16, n_sign, n_mant, n_delta, n_emax);
+  const int rc = check_gemv_args(x, sign, n_sign, mant, n_mant, delta, n_delta, emax, n_emax, tile_off, tile_ent,
+                                 tile_sat, out_f, in_f, mode, y);
   if (rc) return rc;
-  if (in_f % 32 != 0) return BF16X_ESHAPE;
-  if (mode == BF16X_EXACT && (!tile_off || !tile_ent || !tile_sat)) return BF16X_EARG;
-  if (!aligned4(x) || !aligned4(sign) || !aligned4(mant) || !aligned4(delta) || !aligned2(emax) || !aligned2(y))
-    return BF16X_EARG;
   const bool ex = mode == BF16X_EXACT;
-  return launch_gemv_swiglu(x, (const uint32_t*)sign, (const uint32_t*)mant, (const uint32_t*)delta,
-                            (const uint16_t*)emax, ex ? tile_off : nullptr, ex ? tile_ent : nullptr,
-                            ex ? tile_sat : nullptr, out_f, in_f, y, (hipStream_t)stream);
+  return launch_gemv_g1<1, 0>(x, (const uint32_t*)sign, (const uint32_t*)mant, (const uint32_t*)delta,
+                              (const uint16_t*)emax, ex ? tile_off : nullptr, ex ? tile_ent : nullptr,
+                              ex ? tile_sat : nullptr, out_f, in_f, y, NormArgs{nullptr, nullptr, nullptr, 0.f},
+                              (hipStream_t)stream);
+}
+
+extern "C" int bf16x_gemv_norm(const void* x, const uint16_t* residual_in, const uint16_t* norm_weight,
+                               uint16_t* residual_out, float eps, const int32_t* sign, int64_t n_sign,
+                               const int32_t* mant, int64_t n_mant, const int32_t* delta, int64_t n_delta,
+                               const uint8_t* emax, int64_t n_emax, const uint32_t* tile_off,
+                               const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f, int64_t in_f,
+                               int32_t mode, int32_t epilogue, uint16_t* y, bf16x_stream_t stream) {
+  const int rc = check_gemv_args(x, sign, n_sign, mant, n_mant, delta, n_delta, emax, n_emax, tile_off, tile_ent,
+                                 tile_sat, out_f, in_f, mode, y);
+  if (rc) return rc;
+  if (!norm_weight || (epilogue != 0 && epilogue != 1)) return BF16X_EARG;
+  if (!aligned4(norm_weight) || (residual_in && !aligned4(residual_in)) || (residual_out && !aligned4(residual_out)))
+    return BF16X_EARG;
+  if (residual_out && (residual_out == residual_in || (const void*)residual_out == x)) return BF16X_EARG;
+  const bool ex = mode == BF16X_EXACT;
+  const NormArgs na{residual_in, norm_weight, residual_out, eps};
+  const uint32_t *to = ex ? tile_off : nullptr, *te = ex ? tile_ent : nullptr;
+  const uint8_t* ts = ex ? tile_sat : nullptr;
+  if (epilogue == 1)
+    return launch_gemv_g1<1, 1>(x, (const uint32_t*)sign, (const uint32_t*)mant, (const uint32_t*)delta,
+                                (const uint16_t*)emax, to, te, ts, out_f, in_f, y, na, (hipStream_t)stream);
+  return launch_gemv_g1<0, 1>(x, (const uint32_t*)sign, (const uint32_t*)mant, (const uint32_t*)delta,
+                              (const uint16_t*)emax, to, te, ts, out_f, in_f, y, na, (hipStream_t)stream);
 }
 
 extern "C" int bf16x_gemv(const void* x, int32_t x_dtype, const int32_t* sign, int64_t n_sign,

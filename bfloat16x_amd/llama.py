@@ -19,7 +19,9 @@ device-resident state:
   * q/k/v and gate/up are single fused linears, so batch-1 decode runs 4
     GEMVs per layer; gate_up's rows are stored in groups of 8 [gate 4b ..
     4b+3, up 4b .. 4b+3] (pairs8_rows) so that the BF16X gate_up GEMV applies
-    SwiGLU in its epilogue (bf16x_gemv_swiglu): decode runs 7 launches per layer.
+    SwiGLU in its epilogue (bf16x_gemv_swiglu): 7 launches per layer (5 with
+    norm_in_gemv, which folds each RMSNorm into the following GEMV and is
+    off by default: it measured no faster).
 
 Shapes of the benchmark configuration (the defaults of LlamaConfig): 32
 layers, hidden 4096, FFN 14336 (SwiGLU), 32 query / 8 KV heads, head_dim 128,
@@ -237,11 +239,16 @@ def rope_table(max_len: int, theta: float, device) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 # the model
 
-def _swiglu_gemv_ok(mod) -> bool:
-    """A deployed BF16X gate_up the SwiGLU-epilogue GEMV can run."""
+def _norm_gemv_ok(mod) -> bool:
+    """A deployed BF16X linear the one-wave-per-row GEMV variants can run."""
     from .nn import Bf16xFused
     return (isinstance(mod, Bf16xFused) and mod.mode == "fused" and mod._bias is None
-            and mod.in_features <= 4096 and mod.out_features % 8 == 0)
+            and mod.in_features <= 4096)
+
+
+def _swiglu_gemv_ok(mod) -> bool:
+    """A deployed BF16X gate_up the SwiGLU-epilogue GEMV can run."""
+    return _norm_gemv_ok(mod) and mod.out_features % 8 == 0
 
 
 def _device(device):
@@ -305,7 +312,8 @@ class LlamaRunner:
     first token; each decode step consumes `token`, appends one token to the
     history and advances the position."""
 
-    def __init__(self, model: LlamaStack, max_len: int, max_new: int, max_prompt: int | None = None):
+    def __init__(self, model: LlamaStack, max_len: int, max_new: int, max_prompt: int | None = None,
+                 norm_in_gemv: bool = False):
         cfg = model.cfg
         self.model, self.cfg = model, cfg
         dev = model.device
@@ -334,7 +342,46 @@ class LlamaRunner:
         self.fused_decode_attention = attention_decode_supported(cfg.n_heads, cfg.n_kv_heads, self.max_len)
         self.dec_ws = (attention_decode_workspace(cfg.n_heads, cfg.n_kv_heads, self.max_len, dev)
                        if self.fused_decode_attention else None)
+        # norm_in_gemv: decode with the RMSNorms folded into the following GEMVs (bf16x_gemv_norm).  Off by
+        # default: each of the ~900 workgroups of a GEMV recomputes the norm of the whole row before its
+        # first weight row, which costs as much as the standalone RMSNorm launch it saves (measured: gate_up
+        # 40.2 us vs 32.5 + 5.3 us, qkv 14.7 vs 15.3 us; 3.43 vs 3.37 ms/token)
+        self.fused_norm = bool(norm_in_gemv) and self.fused_decode_attention and all(
+            _norm_gemv_ok(lay.qkv) and _swiglu_gemv_ok(lay.gate_up) for lay in model.layers)
+        self.res_a = torch.empty(cfg.hidden, **bf)
+        self.res_b = torch.empty(cfg.hidden, **bf)
+        self.qkv_buf = torch.empty(cfg.qkv_rows, **bf)
         self._prompt_len = 0
+
+    def _decode_fused(self, pos: torch.Tensor, ids: torch.Tensor):
+        """One decode token with every RMSNorm after the first folded into the
+        following GEMV's x staging (bf16x_gemv_norm) and SwiGLU into the
+        gate_up GEMV: per layer qkv GEMV, attention, o GEMV, gate_up GEMV,
+        down GEMV (5 launches).  The residual stream alternates between two
+        one-row buffers (a GEMV stores x + residual to the other one)."""
+        cfg, m = self.cfg, self.model
+        H, KV = cfg.n_heads, cfg.n_kv_heads
+        R = (self.res_a, self.res_b)
+        cur = 0
+        rmsnorm(m.embed, m.layers[0].attn_norm, self.normed, R[0], row_idx=ids, flags=NORM_STORE, eps=cfg.eps)
+        prev = None
+        for i, lay in enumerate(m.layers):
+            q = lay.qkv
+            if i == 0:
+                qkv = q(self.normed[0])
+            else:
+                qkv = ops.bf16x_gemv_norm(prev, R[cur], lay.attn_norm, R[1 - cur], cfg.eps, q._sign, q._mant,
+                                          q._delta, q._emax, q.out_features, q.in_features, plan=q._plan,
+                                          out=self.qkv_buf)
+                cur = 1 - cur
+            attention_decode(qkv, pos, self.cos_sin, H, KV, self.k_cache[i], self.v_cache[i], self.attn, self.dec_ws)
+            o = lay.o(self.attn[0])
+            g = lay.gate_up
+            ops.bf16x_gemv_norm(o, R[cur], lay.mlp_norm, R[1 - cur], cfg.eps, g._sign, g._mant, g._delta, g._emax,
+                                g.out_features, g.in_features, plan=g._plan, swiglu=True, out=self.act[0])
+            cur = 1 - cur
+            prev = lay.down(self.act[0])
+        return prev, R[cur]
 
     # one pass over the stack for `T` tokens starting at position pos[0]
     def _layers(self, T: int, pos: torch.Tensor, ids: torch.Tensor):
@@ -394,6 +441,10 @@ class LlamaRunner:
     @torch.no_grad()
     def step(self) -> None:
         """One eager decode step."""
+        if self.fused_norm:
+            down, res = self._decode_fused(self.state, self.token)
+            self._head(down, res)
+            return
         down = self._layers(1, self.state, self.token)
         self._head(down, self.residual[0])
 

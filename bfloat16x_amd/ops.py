@@ -161,6 +161,39 @@ def bf16x_gemv_swiglu(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan |
     return y
 
 
+def bf16x_gemv_norm(x, residual_in, norm_weight, residual_out, eps, sign, mant, delta, emax, out_f, in_f,
+                    plan: Bf16xPlan | None = None, swiglu: bool = False,
+                    out: torch.Tensor | None = None) -> torch.Tensor:
+    """GEMV whose input is RMSNorm(x + residual_in) * norm_weight, computed in
+    the kernel; x + residual_in is stored to residual_out (include/bf16x_llama.h).
+    swiglu: the SwiGLU epilogue (out_f // 2 outputs)."""
+    s, m, d, e = _streams(sign, mant, delta, emax)
+    out_f, in_f = int(out_f), int(in_f)
+    bf = (torch.bfloat16,)
+    xx = _dev_tensor(x, "x", bf).reshape(-1)
+    nw = _dev_tensor(norm_weight, "norm_weight", bf).reshape(-1)
+    ri = _dev_tensor(residual_in, "residual_in", bf).reshape(-1) if residual_in is not None else None
+    if residual_out is not None and (not residual_out.is_cuda or residual_out.dtype != torch.bfloat16
+                                     or not residual_out.is_contiguous() or residual_out.numel() < in_f):
+        raise ValueError("residual_out must be a contiguous bf16 GPU tensor of in_f elements")
+    for t, nm in ((xx, "x"), (nw, "norm_weight"), (ri, "residual_in")):
+        if t is not None and t.numel() != in_f:
+            raise ValueError(f"{nm} has {t.numel()} elements, in_f = {in_f}")
+    n_out = out_f // 2 if swiglu else out_f
+    y = out if out is not None else torch.empty(n_out, dtype=torch.bfloat16, device=s.device)
+    if y.dtype != torch.bfloat16 or not y.is_contiguous() or y.numel() < n_out:
+        raise ValueError("out must be a contiguous bf16 tensor of the output length")
+    mode = _lib.SATURATED if plan is None else _lib.EXACT
+    st = _lib.lib().bf16x_gemv_norm(xx.data_ptr(), _lib.ptr(ri), nw.data_ptr(), _lib.ptr(residual_out), float(eps),
+                                    s.data_ptr(), s.numel(), m.data_ptr(), m.numel(), d.data_ptr(), d.numel(),
+                                    e.data_ptr(), e.numel(), _lib.ptr(plan.tile_off) if plan else None,
+                                    _lib.ptr(plan.tile_ent) if plan else None,
+                                    _lib.ptr(plan.tile_sat) if plan else None, out_f, in_f, mode,
+                                    1 if swiglu else 0, y.data_ptr(), _lib.stream_of(s.device))
+    _lib.check(st, "bf16x_gemv_norm")
+    return y
+
+
 def bf16x_fused_gemv(x, sign, mant, delta, emax, olk, old, oloff, out_f, in_f, group=16, r=4, bk=256,
                      num_warps=2, *, plan: Bf16xPlan | None = None) -> torch.Tensor:
     """Fused decode+GEMV with the reference's signature (bf16x_fused.py:114).

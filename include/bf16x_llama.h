@@ -104,6 +104,20 @@ int bf16x_gemv_swiglu(const void* x, const int32_t* sign, int64_t n_sign, const 
                       const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
                       int64_t in_f, int32_t mode, uint16_t* out, bf16x_stream_t stream);
 
+/* Fused decode+GEMV whose input is normalised inside the kernel: with
+ * h = bf16(x + residual_in) (h = x when residual_in is NULL), the rows are
+ * multiplied with bf16(bf16(h * rsqrt(mean(h^2) + eps)) * norm_weight), the
+ * bf16x_rmsnorm result; h is stored to residual_out (NULL: not stored; it
+ * must not alias x or residual_in).  epilogue 0: y = the GEMV (out_f values);
+ * 1: the SwiGLU epilogue of bf16x_gemv_swiglu.  One token, in_f <= 4096,
+ * x / residuals / norm_weight 4-byte aligned.  Folds the RMSNorm (and the
+ * residual add) that precedes a projection into it. */
+int bf16x_gemv_norm(const void* x, const uint16_t* residual_in, const uint16_t* norm_weight,
+                    uint16_t* residual_out, float eps, const int32_t* sign, int64_t n_sign, const int32_t* mant,
+                    int64_t n_mant, const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                    const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
+                    int64_t in_f, int32_t mode, int32_t epilogue, uint16_t* y, bf16x_stream_t stream);
+
 /* Greedy step: token[0] = argmax(logits[0 .. vocab)) (the first maximum),
  * history[state[1]] = token[0] when state[1] < history_len, then state[1]++
  * and state[0]++.  logits 16-byte aligned. */

@@ -244,6 +244,37 @@ def test_greedy(bx, V):
     assert hist.tolist() == [V // 3, V // 3] and state.tolist() == [53, 3]
 
 
+@torch.no_grad()
+@pytest.mark.parametrize("out_f,in_f,swiglu,res", [(6144, 4096, False, True), (28672, 4096, True, True),
+                                                  (1024, 512, False, False), (3072, 512, True, True)])
+def test_gemv_norm_matches_unfused(bx, out_f, in_f, swiglu, res):
+    """RMSNorm folded into the GEMV's staging against the RMSNorm kernel
+    followed by the plain (or SwiGLU) GEMV: the stored residual is bit-exact,
+    the products agree to the north-star tolerance (the sum of squares is
+    reduced in another order, so the scale may differ in its last bit)."""
+    from bfloat16x_amd import ops
+    from tests.test_gpu_dict import check_tol
+    bits = dc.bench_weight_bits(out_f, in_f, seed=14)
+    w = torch.from_numpy(bits.view(np.int16).copy()).view(torch.bfloat16)
+    d = bx.bf16x_quantize(w.to(DEV))
+    plan = bx.build_plan_host(d, device=DEV)
+    args = (d["sign_packed"], d["mant_packed"], d["delta_packed"], d["emax"], out_f, in_f)
+    x, r, nw = rnd(in_f, 15).to(DEV), rnd(in_f, 16).to(DEV), rnd(in_f, 17, 0.5).to(DEV)
+    r_out = torch.empty(in_f, dtype=torch.bfloat16, device=DEV)
+    y = ops.bf16x_gemv_norm(x, r if res else None, nw, r_out, 1e-5, *args, plan=plan, swiglu=swiglu)
+    # unfused
+    r2 = r.clone()
+    normed = torch.empty(in_f, dtype=torch.bfloat16, device=DEV)
+    if res:
+        llama.rmsnorm(x, nw, normed, r2, flags=llama.NORM_ADD | llama.NORM_STORE)
+        assert torch.equal(r_out, r2)
+    else:
+        llama.rmsnorm(x, nw, normed)
+        assert torch.equal(r_out, x)
+    y2 = ops.bf16x_gemv_swiglu(normed, *args, plan=plan) if swiglu else ops.bf16x_gemv(normed, *args, plan=plan)
+    check_tol(y.float().cpu().numpy(), y2.double().cpu().numpy())
+
+
 # --------------------------------------------------------------------------- the stack
 
 SMALL = llama.LlamaConfig(n_layers=2, hidden=512, ffn=1536, n_heads=4, n_kv_heads=2, vocab=1000)
@@ -320,6 +351,25 @@ def test_decode_steps_match_prefill_over_same_tokens(small):
     r2.prefill(full.to(DEV))
     assert norm_rel(last, r2.logits.float().cpu().numpy()) < 1e-2
     assert int(r2.history[0]) == toks[-1]
+
+
+@torch.no_grad()
+def test_norm_in_gemv_decode_matches_prefill(small):
+    """The decode step with every RMSNorm folded into the following GEMV
+    (norm_in_gemv) against a prefill over the same tokens, and against the
+    unfused decode."""
+    _, mx, _, ids = small
+    r = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32, norm_in_gemv=True)
+    assert r.fused_norm
+    toks = r.generate(ids.to(DEV), 6, graph=False)
+    last = r.logits.float().cpu().numpy()
+    r2 = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32)
+    r2.prefill(torch.cat([ids, torch.tensor(toks[:-1])]).to(DEV))
+    assert norm_rel(last, r2.logits.float().cpu().numpy()) < 1e-2
+    r3 = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32)
+    assert not r3.fused_norm
+    r3.generate(ids.to(DEV), 6, graph=False)
+    assert norm_rel(last, r3.logits.float().cpu().numpy()) < 1e-2
 
 
 @torch.no_grad()

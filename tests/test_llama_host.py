@@ -82,6 +82,14 @@ def test_entry_points_validate_before_launch():
         _lib.ESHAPE                                                       # in_f > 4096
     ls_, lm_, ld_, le_ = lens(16, 128)
     assert _call("bf16x_gemv_swiglu", p, p, ls_, p, lm_, p, ld_, p, le_, p, p, p, 16, 128, 5, p, None) == _lib.EARG
+    # norm GEMV: missing norm weight, bad epilogue, residual_out aliasing residual_in or x
+    q = p + 4096
+    norm_args = lambda x, ri, w, ro, epi: (x, ri, w, ro, 1e-5, p, ls_, p, lm_, p, ld_, p, le_, p, p, p, 16, 128, 1,
+                                            epi, p, None)
+    assert _call("bf16x_gemv_norm", *norm_args(p, q, None, p + 8192, 0)) == _lib.EARG
+    assert _call("bf16x_gemv_norm", *norm_args(p, q, q, p + 8192, 2)) == _lib.EARG
+    assert _call("bf16x_gemv_norm", *norm_args(p, q, q, q, 0)) == _lib.EARG
+    assert _call("bf16x_gemv_norm", *norm_args(p, q, q, p, 0)) == _lib.EARG
     # greedy: misaligned token, history without length
     assert _call("bf16x_greedy", p, 8, p + 4, p, p, 1, None) == _lib.EARG
     assert _call("bf16x_greedy", p, 8, p, p, None, 1, None) == _lib.EARG
