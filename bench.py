@@ -280,11 +280,21 @@ def main():
                     help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 2048],
                     help="activation rows of the decode+GEMM lines (configuration 3)")
+    ap.add_argument("--only", choices=("llama", "gguf"),
+                    help="run one secondary workload alone and print its record (a measurement / profiling mode, "
+                         "not the benchmark line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
               file=sys.stderr)
         sys.exit(2)
+    if args.only:
+        import bfloat16x_amd as bx
+        dev = torch.device("cuda:0")
+        torch.cuda.set_device(dev)
+        rec = bench_llama(bx, dev) if args.only == "llama" else bench_gguf(bx, dev, torch.cuda.current_stream(dev))
+        print(json.dumps({"only": args.only, "record": rec}), flush=True)
+        return
 
     import bfloat16x_amd as bx
     from bfloat16x_amd import _lib
