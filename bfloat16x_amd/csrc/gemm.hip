@@ -455,7 +455,23 @@ int bf16x_gemm_skinny_launch(const uint16_t* x, int64_t M, const uint32_t* s, co
                              const uint16_t* e, const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f,
                              int64_t in_f, bool exact, bool yf32, void* y, hipStream_t st);
 
+// few-row MFMA kernel (gemm_skinny2.hip): M <= skinny2_rows(), in_f % 128 == 0
+int64_t bf16x_gemm_skinny2_workspace(int64_t M, int64_t out_f, int64_t in_f);
+int bf16x_gemm_skinny2_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m,
+                              const uint32_t* d, const uint16_t* e, const uint32_t* kp_off, const uint32_t* kp_ent,
+                              int64_t out_f, int64_t in_f, bool exact, bool yf32, void* y, void* workspace,
+                              int64_t workspace_bytes, hipStream_t st);
+
 namespace {
+
+// Largest M served by the 16x16x32-MFMA few-row kernel (at most 64).
+int64_t skinny2_rows() {
+  int64_t r = 64;
+  if (const char* e = getenv("BF16X_GEMM_SKINNY2_MAX")) r = atoll(e);
+  return r < 0 ? 0 : (r > 64 ? 64 : r);
+}
+
+bool use_skinny2(int64_t M, int64_t in_f) { return M <= skinny2_rows() && in_f % 128 == 0; }
 
 // Largest M served by the few-row kernel (at most 128, its column-block
 // limit; measured faster than the tiled kernel up to 32 rows).
@@ -500,7 +516,9 @@ GemmShape gemm_shape(int64_t M, int64_t out_f, int64_t in_f) {
 }  // namespace
 
 extern "C" int64_t bf16x_gemm_workspace(int64_t M, int64_t out_f, int64_t in_f) {
-  if (M <= 0 || out_f <= 0 || in_f < kBK || M <= skinny_rows()) return 0;
+  if (M <= 0 || out_f <= 0 || in_f < kBK) return 0;
+  if (use_skinny2(M, in_f)) return bf16x_gemm_skinny2_workspace(M, out_f, in_f);
+  if (M <= skinny_rows()) return 0;
   const GemmShape g = gemm_shape(M, out_f, in_f);
   return g.nsplit > 1 ? (int64_t)g.nsplit * M * out_f * 4 : 0;
 }
@@ -523,6 +541,12 @@ extern "C" int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M, const int32
   if (!aligned4(sign) || !aligned4(mant) || !aligned4(delta) || !aligned2(emax) || !aligned16(x) || !aligned4(y))
     return BF16X_EARG;
   hipStream_t st = (hipStream_t)stream;
+  if (use_skinny2(M, in_f)) {
+    rc = bf16x_gemm_skinny2_launch((const uint16_t*)x, M, (const uint32_t*)sign, (const uint32_t*)mant,
+                                   (const uint32_t*)delta, (const uint16_t*)emax, kp_off, kp_ent, out_f, in_f,
+                                   mode == BF16X_EXACT, y_dtype == BF16X_F32, y, workspace, workspace_bytes, st);
+    return rc ? rc : launch_status();
+  }
   if (M <= skinny_rows()) {
     rc = bf16x_gemm_skinny_launch((const uint16_t*)x, M, (const uint32_t*)sign, (const uint32_t*)mant,
                                   (const uint32_t*)delta, (const uint16_t*)emax, kp_off, kp_ent, out_f, in_f,
