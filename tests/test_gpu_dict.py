@@ -84,7 +84,9 @@ def check_tol(y, y_ref, max_tol=1e-2, med_tol=2e-3):
     return mx, med
 
 
-@pytest.mark.parametrize("shape", [(48, 1536), (2048, 1536), (256, 4096), (40, 14336), (16, 28672)])
+# (2103, 14336): rows split over 4 waves with 4 row groups per workgroup and a
+# ragged last workgroup
+@pytest.mark.parametrize("shape", [(48, 1536), (2048, 1536), (256, 4096), (40, 14336), (16, 28672), (2103, 14336)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float32])
 def test_gemv_exact(bx, shape, xdt):
     print("gemv", shape, xdt, flush=True)
