@@ -29,6 +29,7 @@ Printed as one JSON line; diagnostics go to stderr.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import platform
@@ -64,13 +65,18 @@ def alg_bytes_gemv(d: dict, n_fix: int) -> int:
             + d["emax"].numel() + 5 * n_fix + 2 * d["in_f"] + 2 * d["out_f"])
 
 
-def time_launches(fn, n_launch: int, warmup: int, stream) -> float:
-    """Mean seconds per launch over n_launch back-to-back launches."""
+def time_launches(fn, n_launch: int, warmup: int, stream, queued: bool = False) -> float:
+    """Mean seconds per launch over n_launch back-to-back launches.  queued:
+    a GPU spin first, so the host has enqueued every launch before the first
+    one starts (launches shorter than their host-side call are then timed on
+    the GPU, not on the host)."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
+    if queued:
+        torch.cuda._sleep(20_000_000)
     t0.record(stream)
     for i in range(n_launch):
         fn(i)
@@ -116,6 +122,72 @@ def measured_traffic():
             return json.load(f)["hbm_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def bench_sweep(bx, dev, stream) -> dict:
+    """Configurations 2 and 3 at every shape: fused decode+GEMV (batch 1,
+    exact) against bf16 F.linear, and decode+GEMM (exact; fused kernel and
+    the default dispatch) against bf16 F.linear on the decoded weight, each
+    over rotating weight copies (more bytes than the Infinity Cache holds)."""
+    gemv_rec, gemm_rec = [], []
+    for out_f, in_f in ((4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)):
+        w = bench_weight(out_f, in_f, seed=0)
+        wd = w.to(dev)
+        d = bx.bf16x_quantize(wd)                       # device encoder
+        plan = bx.build_plan_host(d, device=dev)
+        keys = ("sign_packed", "mant_packed", "delta_packed", "emax")
+        comp = sum(d[k].numel() * d[k].element_size() for k in keys) + plan.nbytes
+        nc = max(2, -(-3 * MALL_BYTES // comp))
+        cps = [({k: d[k].clone() for k in keys},
+                dataclasses.replace(plan, tile_off=plan.tile_off.clone(), tile_ent=plan.tile_ent.clone(),
+                                    tile_sat=plan.tile_sat.clone())) for _ in range(nc)]
+        x = torch.randn(in_f, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).to(dev)
+        y = torch.empty(out_f, dtype=torch.bfloat16, device=dev)
+
+        def gv(i):
+            g, p = cps[i % nc]
+            bx.bf16x_gemv(x, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f, plan=p,
+                          out=y)
+
+        sec = time_launches(gv, 200, 20, stream, queued=True)
+        ab = alg_bytes_gemv({"sign_packed": d["sign_packed"], "mant_packed": d["mant_packed"],
+                             "delta_packed": d["delta_packed"], "emax": d["emax"], "in_f": in_f, "out_f": out_f},
+                            plan.n_fix)
+        nw = max(2, -(-3 * MALL_BYTES // (wd.numel() * 2)))
+        wcs = [wd] + [wd.clone() for _ in range(nw - 1)]
+        xb = x.view(1, in_f)
+        sec_b = time_launches(lambda i: torch.nn.functional.linear(xb, wcs[i % nw]), 200, 20, stream, queued=True)
+        ent = {"shape": f"{out_f}x{in_f}", "us": round(sec * 1e6, 2), "GBps": round(ab / sec / 1e9, 1),
+               "hbm_frac": round(ab / sec / 1e9 / HBM_PEAK_GBS, 4), "bf16_linear_us": round(sec_b * 1e6, 2),
+               "speedup_vs_bf16": round(sec_b / sec, 3)}
+        gemv_rec.append(ent)
+        log(f"config2 gemv {ent}")
+        del wcs
+        if (out_f, in_f) != (1024, 4096):
+            for _, p in cps:
+                p.kplan()
+            for M in (16, 64, 256, 512, 2048):
+                xm = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16).to(dev)
+                flops = 2.0 * M * out_f * in_f
+                e = {"shape": f"{out_f}x{in_f}", "M": M}
+                for path in ("fused", "auto"):
+                    def gm(i, path=path):
+                        g, p = cps[i % nc]
+                        bx.bf16x_gemm(xm, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f,
+                                      in_f, plan=p, path=path)
+                    n_l = max(6, min(100, int(0.05 / max(flops / 5e14, 1e-6))))
+                    sg = time_launches(gm, n_l, 3, stream, queued=True)
+                    e[f"{path}_us"] = round(sg * 1e6, 2)
+                    e[f"{path}_tflops"] = round(flops / sg / 1e12, 1)
+                st_ = time_launches(lambda i: torch.nn.functional.linear(xm, wd), 30, 3, stream, queued=True)
+                e["torch_bf16_linear_us"] = round(st_ * 1e6, 2)
+                e["auto_mfma_frac"] = round(flops / (e["auto_us"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+                gemm_rec.append(e)
+                log(f"config3 gemm {e}")
+                del xm
+        del cps, d, plan, wd
+        torch.cuda.empty_cache()
+    return {"gemv_config2": gemv_rec, "gemm_config3": gemm_rec}
 
 
 def bench_gguf(bx, dev, stream) -> list:
@@ -276,11 +348,13 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=7168)
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF (configuration 5) lines")
     ap.add_argument("--no-llama", action="store_true", help="skip the Llama-stack (configuration 4) line")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the configuration-2/3 shape sweep (GEMV at four shapes, GEMM at three x five M)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 2048],
                     help="activation rows of the decode+GEMM lines (configuration 3)")
-    ap.add_argument("--only", choices=("llama", "gguf"),
+    ap.add_argument("--only", choices=("llama", "gguf", "sweep"),
                     help="run one secondary workload alone and print its record (a measurement / profiling mode, "
                          "not the benchmark line)")
     args = ap.parse_args()
@@ -292,7 +366,9 @@ def main():
         import bfloat16x_amd as bx
         dev = torch.device("cuda:0")
         torch.cuda.set_device(dev)
-        rec = bench_llama(bx, dev) if args.only == "llama" else bench_gguf(bx, dev, torch.cuda.current_stream(dev))
+        st_ = torch.cuda.current_stream(dev)
+        rec = (bench_llama(bx, dev) if args.only == "llama" else
+               bench_gguf(bx, dev, st_) if args.only == "gguf" else bench_sweep(bx, dev, st_))
         print(json.dumps({"only": args.only, "record": rec}), flush=True)
         return
 
@@ -418,9 +494,14 @@ def main():
         log(f"gemm {ent}")
         del xm
 
-    # ---- configuration 5: GGUF half-block, 70B-layer shapes, Student-t(3) x 0.015
+    # ---- configurations 2 and 3 at every shape
     del copies, argv
     torch.cuda.empty_cache()
+    sweep_rec = None
+    if not args.no_sweep:
+        sweep_rec = bench_sweep(bx, dev, stream)
+
+    # ---- configuration 5: GGUF half-block, 70B-layer shapes, Student-t(3) x 0.015
     gguf_rec = None
     if not args.no_gguf:
         gguf_rec = bench_gguf(bx, dev, stream)
@@ -461,6 +542,7 @@ def main():
         "decode_exact_14336x4096": decode_rec,
         "device_encoder_14336x4096": enc_rec,
         "gemm_14336x4096_exact": gemm_rec,
+        "config2_config3_sweep": sweep_rec,
         "gguf_config5": gguf_rec,
         "llama_config4": llama_rec,
     }
