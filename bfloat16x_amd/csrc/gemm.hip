@@ -21,7 +21,7 @@
 //     j + 2 is decoded and step j + 1 (decoded one iteration earlier, so every
 //     thread's stores are visible) is patched, with one barrier per step.
 //   * EXACT patches come from the step-major plan: entries grouped by (64-column
-//     step, 32-row group), so the 128 rows of a tile at one step are one
+//     step, 16-row group), so the 128 rows of a tile at one step are one
 //     contiguous run; thread t applies entries t and t + 256 of the run (loaded
 //     one iteration ahead), a loop handles longer runs.
 //   * v_mfma_f32_32x32x16_bf16 with A = x (32 rows x 16 k) and B = W^T (16 k x
@@ -30,8 +30,10 @@
 // B[8*(l/32)+v][l%32]; result register v of lane l is D[8*(v/4)+4*(l/32)+v%4][l%32].
 //
 // Step-major plan (built on the device from the row plan by bf16x_kplan_build):
-//   kp_off uint32 [S*G + 1], S = in_f / 64 steps, G = ceil(out_f / 32) groups;
-//     run (s, g) = [kp_off[s*G + g], kp_off[s*G + g + 1]), ordered by row, column;
+//   kp_off uint32 [S*G2 + 1], S = in_f / 64 steps, G2 = 2 ceil(out_f / 32)
+//     groups of 16 rows; run (s, h) = [kp_off[s*G2 + h], kp_off[s*G2 + h + 1]),
+//     ordered by row, column, so the run of the 32 rows 32g .. 32g+31 is
+//     [kp_off[s*G2 + 2g], kp_off[s*G2 + 2g + 2]);
 //   kp_ent uint32: (row & 255) << 22 | (column & 63) << 16 | exact bf16 bits.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -85,6 +87,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   const int64_t P = in_f >> 5;                  // atoms per row
   const int S = (int)(in_f >> 6);               // steps of 64 columns
   const int G = (int)((out_f + kGroupRows - 1) / kGroupRows);
+  const int G2 = 2 * G;                         // 16-row groups of the plan
 
   // XCD-aware tile order: blocks are dispatched round-robin over 8 XCDs; give
   // each XCD a contiguous run of tiles, M fastest, so the M tiles that share a
@@ -157,17 +160,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   // ---- step-major plan: the run of this tile's rows at a step, its entries
   const int g0 = (int)(n0 / kGroupRows), g1 = min(g0 + BN / kGroupRows, G);
   uint32_t kp_total = 0;
-  if constexpr (EXACT) kp_total = kp_off[(int64_t)S * G];
+  if constexpr (EXACT) kp_total = kp_off[(int64_t)S * G2];
   const __amdgpu_buffer_rsrc_t rent = gemm_rsrc(kp_ent, (uint64_t)kp_total * 4);
   // Bounds are read with vector loads (scalar loads would share lgkmcnt with
   // the LDS operand reads and force a full wait on each of them).
-  const __amdgpu_buffer_rsrc_t roff = gemm_rsrc(kp_off, ((uint64_t)S * G + 1) * 4);
+  const __amdgpu_buffer_rsrc_t roff = gemm_rsrc(kp_off, ((uint64_t)S * G2 + 1) * 4);
   struct Run { uint32_t beg, end, e0, e1; };
   struct Bounds { uint32_t beg, end; };
   auto run_bounds = [&](int j, Bounds& r) {
     const int s = s0 + min(j, n - 1);
-    r.beg = __builtin_amdgcn_raw_buffer_load_b32(roff, (s * G + g0) * 4, 0, 0);
-    r.end = __builtin_amdgcn_raw_buffer_load_b32(roff, (s * G + g1) * 4, 0, 0);
+    r.beg = __builtin_amdgcn_raw_buffer_load_b32(roff, (s * G2 + 2 * g0) * 4, 0, 0);
+    r.end = __builtin_amdgcn_raw_buffer_load_b32(roff, (s * G2 + 2 * g1) * 4, 0, 0);
   };
   auto load_run = [&](const Bounds& bd, Run& r) {   // entries t and t + 256 (reads past the plan return 0)
     r.beg = __builtin_amdgcn_readfirstlane(bd.beg);
@@ -364,34 +367,38 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
 // ---------------------------------------------------------------------------
 // Step-major plan from the row plan (one tile per row, in_f <= 65536).  One
 // 64-lane block per 32-row group; lane r < 32 walks the entries of row
-// g*32 + r, which are sorted by column.  Pass 1 counts each (step, group) run,
-// a one-block scan turns counts into offsets, pass 2 writes the entries.
+// g*32 + r, which are sorted by column; lanes 0-15 and 16-31 make the runs of
+// the 16-row groups 2g and 2g + 1.  Pass 1 counts each (step, 16-row group)
+// run, a one-block scan turns counts into offsets, pass 2 writes the entries.
 // ---------------------------------------------------------------------------
 template <bool FILL>
 __global__ __launch_bounds__(64) void kplan_pass_kernel(const uint32_t* __restrict__ tile_off,
                                                         const uint32_t* __restrict__ tile_ent, int64_t out_f,
-                                                        int S, int G, uint32_t* __restrict__ kp_off,
+                                                        int S, int G2, uint32_t* __restrict__ kp_off,
                                                         uint32_t* __restrict__ kp_ent) {
   const int g = blockIdx.x, lane = threadIdx.x;
+  const int h = 2 * g + (lane >= 16 ? 1 : 0);    // 16-row group of this lane's row
   const int64_t row = (int64_t)g * kGroupRows + lane;
   const bool live = lane < kGroupRows && row < out_f;
   uint32_t p = live ? tile_off[row] : 0, pe = live ? tile_off[row + 1] : 0;
   for (int s = 0; s < S; ++s) {
     uint32_t c = 0;
     while (p + c < pe && (tile_ent[p + c] >> 22) == (uint32_t)s) ++c;   // column >> 6 == s
+    uint32_t incl = c;                   // inclusive prefix over the lanes
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t v = __shfl_up(incl, o);
+      if (lane >= o) incl += v;
+    }
+    const uint32_t lo = __shfl(incl, 15);  // entries of the first 16-row group
+    const uint32_t all = __shfl(incl, 63);
     if constexpr (!FILL) {
-      uint32_t t = c;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) t += __shfl_xor(t, o);
-      if (lane == 0) kp_off[(int64_t)s * G + g] = t;
-    } else {
-      uint32_t incl = c;                 // inclusive prefix over the lanes
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t v = __shfl_up(incl, o);
-        if (lane >= o) incl += v;
+      if (lane == 0) {
+        kp_off[(int64_t)s * G2 + 2 * g] = lo;
+        kp_off[(int64_t)s * G2 + 2 * g + 1] = all - lo;
       }
-      const uint32_t base = kp_off[(int64_t)s * G + g] + incl - c;
+    } else {
+      const uint32_t base = kp_off[(int64_t)s * G2 + h] + (lane >= 16 ? incl - lo : incl) - c;
       for (uint32_t i = 0; i < c; ++i) {
         const uint32_t e = tile_ent[p + i];
         kp_ent[base + i] = ((uint32_t)(row & 255) << 22) | (((e >> 16) & 63u) << 16) | (e & 0xFFFFu);
@@ -432,21 +439,21 @@ using namespace bf16x;
 
 extern "C" int64_t bf16x_kplan_size(int64_t out_f, int64_t in_f) {
   if (out_f <= 0 || in_f < kBK) return 0;
-  return (in_f / kBK) * ((out_f + kGroupRows - 1) / kGroupRows) + 1;
+  return (in_f / kBK) * 2 * ((out_f + kGroupRows - 1) / kGroupRows) + 1;
 }
 
 extern "C" int bf16x_kplan_build(const uint32_t* tile_off, const uint32_t* tile_ent, int64_t out_f, int64_t in_f,
                                  uint32_t* kp_off, uint32_t* kp_ent, bf16x_stream_t stream) {
   if (!tile_off || !tile_ent || !kp_off || !kp_ent) return BF16X_EARG;
   if (out_f <= 0 || in_f <= 0 || (in_f % kBK) != 0 || tiles_per_row(in_f) != 1) return BF16X_ESHAPE;
-  const int64_t S = in_f / kBK, G = (out_f + kGroupRows - 1) / kGroupRows;
-  if (G > INT32_MAX || S * G + 1 > (int64_t)INT32_MAX) return BF16X_ESHAPE;
+  const int64_t S = in_f / kBK, G = (out_f + kGroupRows - 1) / kGroupRows, G2 = 2 * G;
+  if (G2 > INT32_MAX || S * G2 + 1 > (int64_t)INT32_MAX) return BF16X_ESHAPE;
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(kplan_pass_kernel<false>, dim3((unsigned)G), dim3(64), 0, st, tile_off, tile_ent, out_f, (int)S,
-                     (int)G, kp_off, kp_ent);
-  hipLaunchKernelGGL(kplan_scan_kernel, dim3(1), dim3(1024), 0, st, kp_off, S * G);
+                     (int)G2, kp_off, kp_ent);
+  hipLaunchKernelGGL(kplan_scan_kernel, dim3(1), dim3(1024), 0, st, kp_off, S * G2);
   hipLaunchKernelGGL(kplan_pass_kernel<true>, dim3((unsigned)G), dim3(64), 0, st, tile_off, tile_ent, out_f, (int)S,
-                     (int)G, kp_off, kp_ent);
+                     (int)G2, kp_off, kp_ent);
   return launch_status();
 }
 

@@ -127,9 +127,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_skinny_kernel(
   };
 
   // ---- step-major plan run of (step, this group): entries lane, lane + 64
-  const __amdgpu_buffer_rsrc_t roff = rsrc(kp_off, ((uint64_t)S * G + 1) * 4);
+  const __amdgpu_buffer_rsrc_t roff = rsrc(kp_off, ((uint64_t)S * 2 * G + 1) * 4);
   uint32_t kp_total = 0;
-  if constexpr (EXACT) kp_total = kp_off[(int64_t)S * G];
+  if constexpr (EXACT) kp_total = kp_off[(int64_t)S * 2 * G];
   const __amdgpu_buffer_rsrc_t rent = rsrc(kp_ent, (uint64_t)kp_total * 4);
   // run bounds are read two steps before the entries, the entries two steps
   // before their use, all with vector loads issued in consumption order
@@ -137,8 +137,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemm_skinny_kernel(
   struct Run { uint32_t beg, end, e0, e1; };
   auto load_bounds = [&](int j, Bounds& bd) {
     const int s = s0 + min(j, n - 1);
-    bd.bb = __builtin_amdgcn_raw_buffer_load_b32(roff, (s * G + g) * 4, 0, 0);
-    bd.be = __builtin_amdgcn_raw_buffer_load_b32(roff, (s * G + g + 1) * 4, 0, 0);
+    bd.bb = __builtin_amdgcn_raw_buffer_load_b32(roff, (s * 2 * G + 2 * g) * 4, 0, 0);       // 16-row groups
+    bd.be = __builtin_amdgcn_raw_buffer_load_b32(roff, (s * 2 * G + 2 * g + 2) * 4, 0, 0);   // 2g and 2g + 1
   };
   auto load_run = [&](const Bounds& bd, Run& r) {
     r.beg = __builtin_amdgcn_readfirstlane(bd.bb);

@@ -10,8 +10,8 @@
 // The MFMA wants lane l to hold row l % 16 (below), so the decoded words are
 // exchanged through a wave-private LDS scratch: written in load order, read
 // back in MFMA order (LDS operations of one wave complete in issue order).
-// In EXACT mode the step's two plan runs (64-column steps of the 32-row
-// group) are written over the scratch in between.
+// In EXACT mode the step's two plan runs (64-column steps of the wave's
+// 16-row group) are written over the scratch in between.
 //
 // k order.  MFMA i (i < 4) takes pair words 4i .. 4i+3 of atom q = l / 16 of
 // row r = l % 16 as lane l's A fragment: an MFMA sums over its 32 k values in
@@ -54,11 +54,10 @@ constexpr int kStep = 128;                 // columns per step (4 atoms per row)
 constexpr int kRowsWave = 16;
 constexpr int kWaves = 4;
 constexpr int kRowsBlock = kRowsWave * kWaves;
-constexpr int kGroupRows = 32;             // rows per step-major plan group
+constexpr int kGroupRows = 32;             // G counts groups of 32 rows; the plan has 2 G groups of 16
 constexpr int kXStride = 272;              // bytes per token row of the LDS x tile (256 + 16: bank skew)
 constexpr int kScratch = 64 * 64 + 64 * 4; // per-wave patch scratch + one trash word per lane
 constexpr int kMaxRows = 64;               // activation rows served
-constexpr int kDepth = 4;                  // steps of W atoms in flight (even: the x and plan registers alternate)
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint64_t bytes) {
   const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
@@ -70,32 +69,46 @@ struct WAtom {
   uint32_t ew;     // dword holding this atom's emax pair (and its neighbour's)
 };
 struct Bounds { uint32_t b0, e0, b1, e1; };
-struct Ents { uint32_t v[4]; };
+struct Ents { uint32_t v[2]; };
 
-template <int NC, bool EXACT, bool PARTIAL, bool YF32>
-__global__ __launch_bounds__(256) void gemm_skinny2_kernel(
+// KQ waves share each 16-row group and take consecutive 128-column steps of
+// it (a workgroup step is KQ steps): the KQ load instructions that read a
+// row's adjacent segments are issued together, so the L1 fetches each cache
+// line once for all of them (requests to a line already in flight are
+// merged) instead of once per step.  The KQ partial sums of a row group are
+// added in wave order at the end.
+template <int NC, int KQ, bool EXACT, bool PARTIAL, bool YF32>
+__global__ __launch_bounds__(256 * KQ) void gemm_skinny2_kernel(
     const uint16_t* __restrict__ x, int64_t M, const uint32_t* __restrict__ sign,
     const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
     const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent, int64_t out_f, int64_t in_f,
     int sps, void* __restrict__ out) {
+  constexpr int D = KQ == 1 ? 4 : 2;               // workgroup steps of W atoms in flight (even)
+  constexpr int NT = 256 * KQ;                     // threads
   constexpr int MP = NC * 16;                      // tokens padded to whole MFMA blocks
-  constexpr int XBUF = MP * kXStride;
-  constexpr int XI = (MP * 16 + 255) / 256;        // 16-byte x chunks per thread per step
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * XBUF + kWaves * kScratch];
+  constexpr int XROW = 256 * KQ + 16;              // bytes per token row of the LDS x tile (+16: bank skew)
+  constexpr int XBUF = MP * XROW;
+  constexpr int XC = 16 * KQ;                      // 16-byte x chunks per token row
+  constexpr int XI = (MP * XC + NT - 1) / NT;      // x chunks per thread per workgroup step
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * XBUF + kWaves * KQ * kScratch];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wg = wave / KQ, kq = wave - (wave / KQ) * KQ;     // row group, step within the workgroup step
   const int64_t P = in_f >> 5;
   const int S = (int)(in_f / kStep);
   const int G = (int)((out_f + kGroupRows - 1) / kGroupRows);
   const int nb_rows = (int)((out_f + kRowsBlock - 1) / kRowsBlock);
   const int tile = (int)blockIdx.x % nb_rows, split = (int)blockIdx.x / nb_rows;
   const int s0 = split * sps;
-  const int n = max(0, min(sps, S - s0));
+  const int n = max(0, min(sps, S - s0));                     // steps of this workgroup
+  const int nm = (n + KQ - 1) / KQ;                           // workgroup steps
   const int last = max(n - 1, 0);
-  const int64_t n0w = (int64_t)tile * kRowsBlock + wave * kRowsWave;   // this wave's first row
+  const int64_t n0w = (int64_t)tile * kRowsBlock + wg * kRowsWave;      // this wave's first row
   const int r = lane & 15, q = lane >> 4;          // MFMA role: row r, atom q of the step
   const int rl = lane >> 2, ql = lane & 3;         // load role: row rl, atom ql of the step
+  // step (within the split) of this wave at workgroup step m, clamped into it
+  auto wstep = [&](int m) { return min(m * KQ + kq, last); };
 
   // ---- W atoms: lane -> (row n0w + rl, atom 4 s + ql); the step enters as a
   // uniform scalar offset
@@ -107,8 +120,8 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
   const uint32_t av = (uint32_t)(wrow * P) + (uint32_t)ql;
   const uint32_t vo_m = av * 28, vo_d = av * 12, vo_s = av * 4, vo_e = (av & ~1u) * 2;
   const uint32_t esh = 16u * (av & 1u);            // P % 4 == 0: the parity of the atom index is step-invariant
-  auto load_w = [&](int j, WAtom& t) {
-    const uint32_t sa = 4u * (uint32_t)(s0 + min(j, last));
+  auto load_w = [&](int m, WAtom& t) {
+    const uint32_t sa = 4u * (uint32_t)(s0 + wstep(m));
     const u32x4 m03 = __builtin_amdgcn_raw_buffer_load_b128(rm_, (int)vo_m, (int)(sa * 28), 0);
     const u32x3 m46 = __builtin_amdgcn_raw_buffer_load_b96(rm_, (int)(vo_m + 16), (int)(sa * 28), 0);
     const u32x3 d02 = __builtin_amdgcn_raw_buffer_load_b96(rd_, (int)vo_d, (int)(sa * 12), 0);
@@ -120,23 +133,27 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
     t.d[0] = e0; t.d[1] = e1; t.d[2] = e2;
   };
 
-  // ---- x tile in pair order: chunk c = i * 256 + tid is (token c / 16, pair
-  // words 4 (c % 4) .. +3 of atom c % 16 / 4) of the step, made from the
-  // 4 elements at 32a + 4 (c % 4) and the 4 elements 16 further
+  // ---- x tile of a workgroup step (KQ steps) in pair order: chunk c = i * NT
+  // + tid is (token c / XC, pair words 4 (c % 4) .. +3 of atom c % XC / 4),
+  // made from the 4 elements at 32a + 4 (c % 4) and the 4 elements 16 further.
+  // The tile starts at the workgroup step's first step; its steps past the
+  // split are not multiplied (their columns may lie past the row: buffer
+  // reads past x return 0, other reads stay inside x).
   const __amdgpu_buffer_rsrc_t rx_ = rsrc(x, (uint64_t)M * in_f * 2);
   uint32_t vx[XI];
   int xs_off[XI];
 #pragma unroll
   for (int i = 0; i < XI; ++i) {
-    const int c = i * 256 + tid;
-    const int tok = min(c >> 4, MP - 1);
+    const int c = i * NT + tid;
+    const int tok = min(c / XC, MP - 1);
     const int64_t tg = min((int64_t)tok, M - 1);
-    vx[i] = (uint32_t)(tg * in_f * 2 + ((c & 15) >> 2) * 64 + (c & 3) * 8);
-    xs_off[i] = tok * kXStride + (c & 15) * 16;
+    const int cr = c % XC;
+    vx[i] = (uint32_t)(tg * in_f * 2 + (cr >> 2) * 64 + (cr & 3) * 8);
+    xs_off[i] = tok * XROW + cr * 16;
   }
   struct XRaw { u32x2a lo, hi; };
-  auto load_x = [&](int j, XRaw (&xr)[XI]) {
-    const uint32_t ks = (uint32_t)(s0 + min(j, last)) * (kStep * 2);
+  auto load_x = [&](int m, XRaw (&xr)[XI]) {
+    const uint32_t ks = (uint32_t)(s0 + min(m * KQ, last)) * (kStep * 2);
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
       const u32x2 a = __builtin_amdgcn_raw_buffer_load_b64(rx_, (int)vx[i], (int)ks, 0);
@@ -149,7 +166,7 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
   auto store_x = [&](const XRaw (&xr)[XI], uint8_t* xb) {
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
-      if (i * 256 + tid < MP * 16) {
+      if (i * NT + tid < MP * XC) {
         const uint32_t l0 = xr[i].lo.x, l1 = xr[i].lo.y, h0 = xr[i].hi.x, h1 = xr[i].hi.y;
         *(u32x4*)(xb + xs_off[i]) = u32x4{perm(h0, l0, 0x05040100u), perm(h0, l0, 0x07060302u),
                                           perm(h1, l1, 0x05040100u), perm(h1, l1, 0x07060302u)};
@@ -157,28 +174,26 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
     }
   };
 
-  // ---- plan: runs (2 s, g32) and (2 s + 1, g32); entries of the other half
-  // of the 32-row group go to the lane's trash word
-  const int g32 = (int)(n0w / kGroupRows), half = (int)((n0w / kRowsWave) & 1);
+  // ---- plan: runs (2 s, h) and (2 s + 1, h) of this wave's step s and
+  // 16-row group h: exactly this wave's rows
+  const int G2 = 2 * G, h16 = (int)(n0w / kRowsWave);
   uint32_t kp_total = 0;
-  if constexpr (EXACT) kp_total = kp_off[(int64_t)2 * S * G];
-  const __amdgpu_buffer_rsrc_t roff = rsrc(kp_off, ((uint64_t)2 * S * G + 1) * 4);
+  if constexpr (EXACT) kp_total = kp_off[(int64_t)2 * S * G2];
+  const __amdgpu_buffer_rsrc_t roff = rsrc(kp_off, ((uint64_t)2 * S * G2 + 1) * 4);
   const __amdgpu_buffer_rsrc_t rent = rsrc(kp_ent, (uint64_t)kp_total * 4);
-  auto load_bounds = [&](int j, Bounds& b) {
-    const int s = s0 + min(j, last);
-    const int o0 = ((2 * s) * G + g32) * 4, o1 = ((2 * s + 1) * G + g32) * 4;
+  auto load_bounds = [&](int m, Bounds& b) {
+    const int s = s0 + wstep(m);
+    const int o0 = ((2 * s) * G2 + h16) * 4, o1 = ((2 * s + 1) * G2 + h16) * 4;
     b.b0 = __builtin_amdgcn_raw_buffer_load_b32(roff, o0, 0, 0);
     b.e0 = __builtin_amdgcn_raw_buffer_load_b32(roff, o0 + 4, 0, 0);
     b.b1 = __builtin_amdgcn_raw_buffer_load_b32(roff, o1, 0, 0);
     b.e1 = __builtin_amdgcn_raw_buffer_load_b32(roff, o1 + 4, 0, 0);
   };
-  // entries lane and lane + 64 of each run (reads past the plan return 0)
+  // entry `lane` of each run (reads past the plan return 0)
   auto load_ents = [&](const Bounds& b, Ents& en) {
     const uint32_t b0 = __builtin_amdgcn_readfirstlane(b.b0), b1 = __builtin_amdgcn_readfirstlane(b.b1);
     en.v[0] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((b0 + (uint32_t)lane) * 4), 0, 0);
-    en.v[1] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((b0 + 64u + (uint32_t)lane) * 4), 0, 0);
-    en.v[2] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((b1 + (uint32_t)lane) * 4), 0, 0);
-    en.v[3] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((b1 + 64u + (uint32_t)lane) * 4), 0, 0);
+    en.v[1] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((b1 + (uint32_t)lane) * 4), 0, 0);
   };
   // ---- scratch: slot t = row + 16 * atom (the MFMA lane of that row and
   // atom) holds the 16 pair words in four 16-byte chunks; chunk k sits at
@@ -199,7 +214,7 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
     const int col = (int)((e >> 16) & 63) + 64 * which;
     const int t = (rg & 15) + 16 * (col >> 5);
     const int el = col & 31;
-    uint8_t* dst = (live && (rg >> 4) == half) ? chunk(t, (el & 15) >> 2) + 4 * (el & 3) + 2 * (el >> 4) : trash;
+    uint8_t* dst = live ? chunk(t, (el & 15) >> 2) + 4 * (el & 3) + 2 * (el >> 4) : trash;
     *(uint16_t*)dst = (uint16_t)(e & 0xFFFFu);
   };
 
@@ -207,12 +222,13 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
 #pragma unroll
   for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Step j: decode atoms j (issued kDepth steps ago), patch with the entries of
-  // j (issued one step ago, bounds bc); issue entries j+1 (bounds bn, read one
-  // step ago), bounds j+2 (into bc), atoms j+kDepth (into at); MFMAs from the LDS x
-  // tile of j; x of j+1 (registers xs) to the other LDS buffer, then x of j+3
+  // Workgroup step m: decode this wave's atoms of m (issued D workgroup steps
+  // ago), patch with the entries of m (issued one step ago, bounds bc); issue
+  // entries m+1 (bounds bn, read one step ago), bounds m+2 (into bc), atoms
+  // m+D (into at); MFMAs from the LDS x tile of m (skipped for a step past the
+  // split); x of m+1 (registers xs) to the other LDS buffer, then x of m+3
   // into xs; barrier.
-  auto step = [&](int j, WAtom& at, XRaw (&xs)[XI], Ents& ec, Ents& en, Bounds& bc, const Bounds& bn) {
+  auto step = [&](int m, WAtom& at, XRaw (&xs)[XI], Ents& ec, Ents& en, Bounds& bc, const Bounds& bn) {
     uint32_t w[16];
     {
       Atom t;
@@ -232,11 +248,9 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
       const uint32_t b0 = __builtin_amdgcn_readfirstlane(bc.b0), e0 = __builtin_amdgcn_readfirstlane(bc.e0);
       const uint32_t b1 = __builtin_amdgcn_readfirstlane(bc.b1), e1 = __builtin_amdgcn_readfirstlane(bc.e1);
       patch(ec.v[0], 0, b0 + (uint32_t)lane < e0);
-      patch(ec.v[1], 0, b0 + 64u + (uint32_t)lane < e0);
-      patch(ec.v[2], 1, b1 + (uint32_t)lane < e1);
-      patch(ec.v[3], 1, b1 + 64u + (uint32_t)lane < e1);
-      for (uint32_t e = b0 + 128u + (uint32_t)lane; e < e0; e += 64) patch(kp_ent[e], 0, true);   // dense runs (rare)
-      for (uint32_t e = b1 + 128u + (uint32_t)lane; e < e1; e += 64) patch(kp_ent[e], 1, true);
+      patch(ec.v[1], 1, b1 + (uint32_t)lane < e1);
+      for (uint32_t e = b0 + 64u + (uint32_t)lane; e < e0; e += 64) patch(kp_ent[e], 0, true);   // dense runs (rare)
+      for (uint32_t e = b1 + 64u + (uint32_t)lane; e < e1; e += 64) patch(kp_ent[e], 1, true);
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -250,33 +264,35 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (EXACT) {
       load_ents(bn, en);
-      load_bounds(j + 2, bc);
+      load_bounds(m + 2, bc);
     }
-    load_w(j + kDepth, at);
+    load_w(m + D, at);
     __builtin_amdgcn_sched_barrier(0);
-    const uint8_t* xb = lds + (j & 1) * XBUF;
+    if (KQ == 1 || m * KQ + kq < n) {
+      const uint8_t* xb = lds + (m & 1) * XBUF + 256 * kq;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      bf16x8_t a;
-      const uint32_t aw[4] = {w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
-      __builtin_memcpy(&a, aw, 16);
+      for (int i = 0; i < 4; ++i) {
+        bf16x8_t a;
+        const uint32_t aw[4] = {w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]};
+        __builtin_memcpy(&a, aw, 16);
 #pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        const bf16x8_t b = *(const bf16x8_t*)(xb + (16 * c + r) * kXStride + (16 * q + 4 * i) * 4);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[c], 0, 0, 0);
+        for (int c = 0; c < NC; ++c) {
+          const bf16x8_t b = *(const bf16x8_t*)(xb + (16 * c + r) * XROW + (16 * q + 4 * i) * 4);
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[c], 0, 0, 0);
+        }
       }
     }
-    store_x(xs, lds + ((j + 1) & 1) * XBUF);
+    store_x(xs, lds + ((m + 1) & 1) * XBUF);
     __builtin_amdgcn_sched_barrier(0);
-    load_x(j + 3, xs);
+    load_x(m + 3, xs);
     __syncthreads();
     __builtin_amdgcn_sched_barrier(0);
   };
 
   // ---- prologue: x(0) to LDS; then the loads in flight at the loop entry in
-  // the order steps -kDepth .. -1 would have issued them: atoms 0 .. kDepth-2,
-  // x 1, entries 0, bounds 1, atoms kDepth-1, x 2
-  WAtom A[kDepth];
+  // the order steps -D .. -1 would have issued them: atoms 0 .. D-2, x 1,
+  // entries 0, bounds 1, atoms D-1, x 2
+  WAtom A[D];
   Bounds Bd[2] = {};
   Ents E[2] = {};
   XRaw X[2][XI];
@@ -285,30 +301,50 @@ __global__ __launch_bounds__(256) void gemm_skinny2_kernel(
   store_x(X[0], lds);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int u = 0; u + 1 < kDepth; ++u) load_w(u, A[u]);
+  for (int u = 0; u + 1 < D; ++u) load_w(u, A[u]);
   load_x(1, X[1]);
   __builtin_amdgcn_sched_barrier(0);
   if constexpr (EXACT) {
     load_ents(Bd[0], E[0]);
     load_bounds(1, Bd[1]);
   }
-  load_w(kDepth - 1, A[kDepth - 1]);
+  load_w(D - 1, A[D - 1]);
   load_x(2, X[0]);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
-  // registers at step j: atoms in A[j % kDepth], x of j+1 in X[(j+1) % 2],
-  // entries of j in E[j % 2], bounds of j in Bd[j % 2] and of j+1 in the other
-  int j = 0;
-  for (; j + kDepth - 1 < n; j += kDepth) {
+  // registers at workgroup step m: atoms in A[m % D], x of m+1 in
+  // X[(m+1) % 2], entries of m in E[m % 2], bounds of m in Bd[m % 2] and of
+  // m+1 in the other
+  int m = 0;
+  for (; m + D - 1 < nm; m += D) {
 #pragma unroll
-    for (int u = 0; u < kDepth; ++u) step(j + u, A[u], X[(u + 1) & 1], E[u & 1], E[(u + 1) & 1], Bd[u & 1], Bd[(u + 1) & 1]);
+    for (int u = 0; u < D; ++u) step(m + u, A[u], X[(u + 1) & 1], E[u & 1], E[(u + 1) & 1], Bd[u & 1], Bd[(u + 1) & 1]);
   }
 #pragma unroll
-  for (int u = 0; u + 1 < kDepth; ++u)
-    if (j + u < n) step(j + u, A[u], X[(u + 1) & 1], E[u & 1], E[(u + 1) & 1], Bd[u & 1], Bd[(u + 1) & 1]);
+  for (int u = 0; u + 1 < D; ++u)
+    if (m + u < nm) step(m + u, A[u], X[(u + 1) & 1], E[u & 1], E[(u + 1) & 1], Bd[u & 1], Bd[(u + 1) & 1]);
+  if (n == 0) return;
+
+  // ---- the KQ waves of a row group add their sums in wave order
+  if constexpr (KQ > 1) {
+    float* red = (float*)lds;                      // [row group][kq - 1][NC * 4][64] (the x buffers are free)
+    if (kq > 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) red[((wg * (KQ - 1) + kq - 1) * NC * 4 + c * 4 + v) * 64 + lane] = acc[c][v];
+    }
+    __syncthreads();
+    if (kq > 0) return;
+#pragma unroll
+    for (int k = 1; k < KQ; ++k)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[c][v] += red[((wg * (KQ - 1) + k - 1) * NC * 4 + c * 4 + v) * 64 + lane];
+  }
 
   // ---- results: D[4(l/16) + v][l % 16] = W row n0w + 4q + v, token 16c + r
-  if (n == 0) return;
   const int64_t row0 = n0w + 4 * q;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
@@ -341,43 +377,62 @@ struct Split {
   int sps, ks;
 };
 
-// Workgroups of the (NC, EXACT) kernel resident at once on the current
+// Token blocks of 16 and waves per row group for M activation rows: KQ = 4
+// up to 32 rows (16 waves per workgroup), 1 above (the x tile of 4 steps for
+// 64 tokens would not fit beside the scratch).
+int nc_for(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+int kq_for(int64_t M) {
+  if (const char* e = getenv("BF16X_SKINNY2_KQ")) return atoi(e) == 1 ? 1 : (nc_for(M) <= 2 ? 4 : 1);
+  return nc_for(M) <= 2 ? 4 : 1;
+}
+
+// Workgroups of the (NC, KQ, EXACT) kernel resident at once on the current
 // device, from the runtime's occupancy calculation (registers and LDS of the
-// compiled kernel); 3 per CU on 256 CUs when there is no device to ask.
-template <int NC, bool EXACT>
+// compiled kernel); 3 (KQ = 1) or 1 (KQ = 4) per CU on 256 CUs when there is
+// no device to ask.
+template <int NC, int KQ, bool EXACT>
 int64_t resident_slots() {
   static int64_t cache[64];
+  const int64_t dflt = KQ == 1 ? 768 : 256;
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 768;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return dflt;
   if (cache[dev] > 0) return cache[dev];
   int per_cu = 0, cus = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemm_skinny2_kernel<NC, EXACT, true, false>, 256, 0) !=
-          hipSuccess ||
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemm_skinny2_kernel<NC, KQ, EXACT, true, false>,
+                                                   256 * KQ, 0) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || per_cu <= 0 || cus <= 0)
-    return 768;
+    return dflt;
   cache[dev] = (int64_t)per_cu * cus;
   return cache[dev];
 }
 
 int64_t slots_for(int64_t M, bool exact) {
-  const int nc = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  if (nc == 1) return exact ? resident_slots<1, true>() : resident_slots<1, false>();
-  if (nc == 2) return exact ? resident_slots<2, true>() : resident_slots<2, false>();
-  return exact ? resident_slots<4, true>() : resident_slots<4, false>();
+  const int nc = nc_for(M), kq = kq_for(M);
+  if (kq == 4) {
+    if (nc == 1) return exact ? resident_slots<1, 4, true>() : resident_slots<1, 4, false>();
+    return exact ? resident_slots<2, 4, true>() : resident_slots<2, 4, false>();
+  }
+  if (nc == 1) return exact ? resident_slots<1, 1, true>() : resident_slots<1, 1, false>();
+  if (nc == 2) return exact ? resident_slots<2, 1, true>() : resident_slots<2, 1, false>();
+  return exact ? resident_slots<4, 1, true>() : resident_slots<4, 1, false>();
 }
 
 // K split: as many splits as keep the grid within one round of resident
-// workgroups, at least 2 steps each.  A second, partial round would cost a
-// whole workgroup lifetime for a few workgroups.
+// workgroups, at least 2 workgroup steps each, steps per split a multiple of
+// KQ.  A second, partial round would cost a whole workgroup lifetime for a
+// few workgroups.
 Split skinny2_split(int64_t M, int64_t out_f, int64_t in_f, bool exact) {
   const int64_t tiles = (out_f + kRowsBlock - 1) / kRowsBlock;
   const int64_t S = in_f / kStep;
+  const int64_t kq = kq_for(M);
   int64_t ks = slots_for(M, exact) / tiles;
-  ks = std::max<int64_t>(1, std::min<int64_t>(ks, S / 2));
+  ks = std::max<int64_t>(1, std::min<int64_t>(ks, S / (2 * kq)));
   if (const char* e = getenv("BF16X_SKINNY2_SPLIT")) ks = std::max<int64_t>(1, std::min<int64_t>(atoll(e), S));
   Split sp;
-  sp.sps = (int)((S + ks - 1) / ks);
-  sp.ks = (int)((S + sp.sps - 1) / sp.sps);
+  int64_t sps = (S + ks - 1) / ks;
+  sps = (sps + kq - 1) / kq * kq;
+  sp.sps = (int)sps;
+  sp.ks = (int)((S + sps - 1) / sps);
   return sp;
 }
 
@@ -410,27 +465,32 @@ int bf16x_gemm_skinny2_launch(const uint16_t* x, int64_t M, const uint32_t* s, c
   if (grid > INT32_MAX) return BF16X_ESHAPE;
   float* part = (float*)workspace;
   void* out = partial ? (void*)part : y;
-  const int nc = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-#define BF16X_S2(NC_, EX_, PA_, YF_)                                                                           \
-  hipLaunchKernelGGL((gemm_skinny2_kernel<NC_, EX_, PA_, YF_>), dim3((unsigned)grid), dim3(256), 0, st, x, M, s,  \
-                     m, d, e, kp_off, kp_ent, out_f, in_f, sp.sps, out)
-#define BF16X_S2_NC(NC_)                                                                                  \
+  const int nc = nc_for(M), kq = kq_for(M);
+#define BF16X_S2(NC_, KQ_, EX_, PA_, YF_)                                                                    \
+  hipLaunchKernelGGL((gemm_skinny2_kernel<NC_, KQ_, EX_, PA_, YF_>), dim3((unsigned)grid), dim3(256 * KQ_), 0, st, \
+                     x, M, s, m, d, e, kp_off, kp_ent, out_f, in_f, sp.sps, out)
+#define BF16X_S2_NC(NC_, KQ_)                                                                             \
   do {                                                                                                   \
     if (partial) {                                                                                       \
-      if (exact) BF16X_S2(NC_, true, true, false);                                                       \
-      else BF16X_S2(NC_, false, true, false);                                                            \
+      if (exact) BF16X_S2(NC_, KQ_, true, true, false);                                                  \
+      else BF16X_S2(NC_, KQ_, false, true, false);                                                       \
     } else if (exact) {                                                                                  \
-      if (yf32) BF16X_S2(NC_, true, false, true);                                                        \
-      else BF16X_S2(NC_, true, false, false);                                                            \
+      if (yf32) BF16X_S2(NC_, KQ_, true, false, true);                                                   \
+      else BF16X_S2(NC_, KQ_, true, false, false);                                                       \
     } else {                                                                                             \
-      if (yf32) BF16X_S2(NC_, false, false, true);                                                       \
-      else BF16X_S2(NC_, false, false, false);                                                           \
+      if (yf32) BF16X_S2(NC_, KQ_, false, false, true);                                                  \
+      else BF16X_S2(NC_, KQ_, false, false, false);                                                      \
     }                                                                                                    \
   } while (0)
-  switch (nc) {
-    case 1: BF16X_S2_NC(1); break;
-    case 2: BF16X_S2_NC(2); break;
-    default: BF16X_S2_NC(4); break;
+  if (kq == 4) {
+    if (nc == 1) BF16X_S2_NC(1, 4);
+    else BF16X_S2_NC(2, 4);
+  } else {
+    switch (nc) {
+      case 1: BF16X_S2_NC(1, 1); break;
+      case 2: BF16X_S2_NC(2, 1); break;
+      default: BF16X_S2_NC(4, 1); break;
+    }
   }
 #undef BF16X_S2_NC
 #undef BF16X_S2

@@ -162,9 +162,10 @@ int bf16x_gemv(const void* x, int32_t x_dtype,
  * reference GEMM has no overflow correction, bf16x_gemm_fused.py:9-12).
  * Built on the device from the row plan (tile_off / tile_ent of
  * bf16x_plan_host or bf16x_plan_from_csr): entries regrouped by (64-column
- * step s, 32-row group g).  kp_off: uint32 [bf16x_kplan_size(out_f, in_f)]
- * = [S*G + 1] with S = in_f/64, G = ceil(out_f/32); kp_ent: uint32
- * [n_fix], (row & 255) << 22 | (col & 63) << 16 | exact bf16 bits.
+ * step s, 16-row group h), run (s, h) = [kp_off[s*G2 + h], kp_off[s*G2 + h
+ * + 1]).  kp_off: uint32 [bf16x_kplan_size(out_f, in_f)] = [S*G2 + 1] with
+ * S = in_f/64, G2 = 2 ceil(out_f/32); kp_ent: uint32 [n_fix],
+ * (row & 255) << 22 | (col & 63) << 16 | exact bf16 bits.
  * Requires in_f % 64 == 0 and in_f <= 65536.  All pointers dev.
  * ------------------------------------------------------------------------ */
 int64_t bf16x_kplan_size(int64_t out_f, int64_t in_f);
