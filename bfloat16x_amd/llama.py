@@ -174,8 +174,9 @@ def attention_decode_workspace(n_heads, n_kv_heads, max_len, device) -> torch.Te
 
 
 def attention_decode(qkv, pos, cos_sin, n_heads, n_kv_heads, k_cache, v_cache, out, workspace, scale=None):
-    """One decode token: rope_kv + attention (tokens = 1) in one launch, the
-    keys split over workgroups that combine through `workspace`
+    """One decode token: rope_kv + attention (tokens = 1) in one launch.  Up to
+    256 cache rows one workgroup per KV head takes all keys; longer caches
+    split the keys over workgroups that combine through `workspace`
     (attention_decode_workspace)."""
     for t, nm in ((qkv, "qkv"), (k_cache, "k_cache"), (v_cache, "v_cache"), (out, "out")):
         _bf16_dev(t, nm)
