@@ -77,8 +77,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   static_assert(BN == kBN, "one atom per thread per step");
   constexpr int X_BYTES = BM * kRowBytes;
   constexpr int W_BYTES = BN * kRowBytes;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * X_BYTES + 3 * W_BYTES + 512];   // + patch trash slots
-  uint8_t* const trash = lds + 2 * X_BYTES + 3 * W_BYTES;
+  // 80 KB at 128 x 128: two blocks per CU
+  __shared__ __attribute__((aligned(16))) uint8_t lds[2 * X_BYTES + 3 * W_BYTES];
   uint8_t* const wbase = lds + 2 * X_BYTES;
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -178,19 +178,22 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     r.e0 = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((r.beg + tid) * 4), 0, 0);
     r.e1 = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((r.beg + tid + 256) * 4), 0, 0);
   };
-  // Entries past the run's end go to this thread's trash slot: the store is
+  // Entries past the run's end go to a trash slot: the store is
   // unconditional, so the entry is not first used under a divergent branch
-  // (which would make the compiler wait for every outstanding load).
-  auto patch_one = [&](uint32_t e, uint8_t* wb, bool live) {
+  // (which would make the compiler wait for every outstanding load).  The
+  // slot is the first bytes of this thread's own chunk of the x buffer that
+  // it fills later in the same iteration (free until then, and overwritten
+  // by that store in program order).
+  auto patch_one = [&](uint32_t e, uint8_t* wb, uint8_t* trash, bool live) {
     const int r = (int)(e >> 22) & (BN - 1), c = (int)(e >> 16) & 63;
-    uint8_t* dst = live ? wb + r * kRowBytes + swz(r, c >> 3) * 16 + (c & 7) * 2 : trash + 2 * tid;
+    uint8_t* dst = live ? wb + r * kRowBytes + swz(r, c >> 3) * 16 + (c & 7) * 2 : trash;
     *(uint16_t*)dst = (uint16_t)(e & 0xFFFFu);
   };
-  auto apply_run = [&](const Run& r, uint8_t* wb) {
-    patch_one(r.e0, wb, r.beg + tid < r.end);
-    patch_one(r.e1, wb, r.beg + tid + 256 < r.end);
+  auto apply_run = [&](const Run& r, uint8_t* wb, uint8_t* trash) {
+    patch_one(r.e0, wb, trash, r.beg + tid < r.end);
+    patch_one(r.e1, wb, trash, r.beg + tid + 256 < r.end);
     for (uint32_t e = r.beg + 512 + tid; e < r.end; e += 256)   // dense runs (rare)
-      patch_one(kp_ent[e], wb, true);
+      patch_one(kp_ent[e], wb, trash, true);
   };
 
   // ---- x tile: 16-byte chunk c = i*256 + tid of the step's BM x 64 tile is
@@ -292,7 +295,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
   if constexpr (EXACT) {
-    apply_run(R0, wbase);
+    apply_run(R0, wbase, lds + X_BYTES + xs_off);   // x buffer 1 is first filled in iteration 0
     __syncthreads();
   }
 
@@ -316,7 +319,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(
     __builtin_amdgcn_sched_barrier(0);
     mfma_step(lds + (j & 1) * X_BYTES, wbase + wcur);
     store_w(at, wbase + w2);
-    if constexpr (EXACT) apply_run(Rp, wbase + w1);
+    if constexpr (EXACT) apply_run(Rp, wbase + w1, lds + ((j + 1) & 1) * X_BYTES + xs_off);
     store_x(xr, lds + ((j + 1) & 1) * X_BYTES);
     __builtin_amdgcn_sched_barrier(0);
     load_x(j + 3, xr);
@@ -505,7 +508,7 @@ GemmShape gemm_shape(int64_t M, int64_t out_f, int64_t in_f) {
   if (const char* e = getenv("BF16X_GEMM_BM")) g.bm = atoi(e);
   const int64_t S = in_f / kBK;
   const int64_t tiles = ((M + g.bm - 1) / g.bm) * ((out_f + kBN - 1) / kBN);
-  const int64_t slots = 256 * (g.bm <= 64 ? 2 : 1);
+  const int64_t slots = 256 * (g.bm <= 128 ? 2 : 1);   // resident blocks (LDS: 66 / 80 / 112 KB)
   int best = 1;
   double best_cost = 1e30;
   for (int k = 1; k <= 32 && k * 4 <= S; ++k) {

@@ -197,13 +197,13 @@ __global__ __launch_bounds__(256 * KQ) void gemm_skinny2_kernel(
   };
   // ---- scratch: slot t = row + 16 * atom (the MFMA lane of that row and
   // atom) holds the 16 pair words in four 16-byte chunks; chunk k sits at
-  // position k ^ (t / 2 % 4) ^ (t / 16), so that the 8 lanes an LDS cycle
-  // serves hit 8 different 16-byte bank groups both when written in load
-  // order (slots r + 16 * {0..3} of two rows) and when read in MFMA order
-  // (8 consecutive slots)
+  // position k ^ (t / 4 % 4) ^ (t / 16), so that the 16 lanes an LDS cycle
+  // serves for a 16-byte access hit 16 different 16-byte bank groups both
+  // when written in load order (slots r + 16 * {0..3} of four rows) and when
+  // read in MFMA order (16 consecutive slots)
   uint8_t* scr = lds + 2 * XBUF + wave * kScratch;
   uint8_t* trash = scr + 64 * 64 + lane * 4;
-  auto chunk = [&](int t, int k) { return scr + t * 64 + ((k ^ (t >> 1) ^ (t >> 4)) & 3) * 16; };
+  auto chunk = [&](int t, int k) { return scr + t * 64 + ((k ^ (t >> 2) ^ (t >> 4)) & 3) * 16; };
   // entry (row & 255) << 22 | (column in its 64-column step) << 16 | bits, of
   // run `which`: element (row % 16, column) of the 128-column step is pair
   // word column % 16, half (column % 32) / 16, of slot row % 16 + 16 *
