@@ -85,22 +85,24 @@ def time_launches(fn, n_launch: int, warmup: int, stream, queued: bool = False) 
     return t0.elapsed_time(t1) / 1e3 / n_launch
 
 
-def cpu_baseline(d: dict, alg_bytes_full: int, rows: int) -> dict:
+def cpu_baseline(d: dict, alg_bytes_full: int, rows: int, reps: int) -> dict:
     """The reference's CPU decode+matmul path (restated in oracle/cpu_path.py)
-    on the first `rows` rows, scaled to compressed GB/s."""
+    on the first `rows` rows, median of `reps` timed passes after one warm-up
+    (about 13 s of CPU work at the defaults), scaled to compressed GB/s."""
     from oracle.cpu_path import CpuBf16xLinear
     torch.set_num_threads(os.cpu_count() or 1)
     lin = CpuBf16xLinear(d, tile=1024)
     x = torch.randn(1, d["in_f"], generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
     lin.forward(x, rows=rows)  # warm-up
     ts = []
-    for _ in range(3):
+    for _ in range(reps):
         t = time.perf_counter()
         lin.forward(x, rows=rows)
         ts.append(time.perf_counter() - t)
     ts.sort()
     frac = rows / d["out_f"]
-    gbs = alg_bytes_full * frac / ts[1] / 1e9
+    med = ts[len(ts) // 2]
+    gbs = alg_bytes_full * frac / med / 1e9
     cpu = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as f:
@@ -108,8 +110,9 @@ def cpu_baseline(d: dict, alg_bytes_full: int, rows: int) -> dict:
     except Exception:
         pass
     return {"value": round(gbs, 4), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"first {rows} of {d['out_f']} rows (decode+matmul, batch 1, median of 3 after 1 warm-up)",
-            "seconds_per_sample": round(ts[1], 4), "cpu": cpu}
+            "sample": f"{rows} of {d['out_f']} rows (decode+matmul, batch 1), median of {reps} passes after 1 "
+                      f"warm-up, {sum(ts):.1f} s timed",
+            "seconds_per_sample": round(med, 4), "cpu": cpu}
 
 
 def measured_traffic():
@@ -345,7 +348,8 @@ def main():
     ap.add_argument("--steps", type=int, default=2000)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-rows", type=int, default=7168)
+    ap.add_argument("--cpu-rows", type=int, default=14336)
+    ap.add_argument("--cpu-reps", type=int, default=9)
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF (configuration 5) lines")
     ap.add_argument("--no-llama", action="store_true", help="skip the Llama-stack (configuration 4) line")
     ap.add_argument("--no-sweep", action="store_true",
@@ -514,7 +518,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         t = time.time()
-        cpu = cpu_baseline(d, abytes, args.cpu_rows)
+        cpu = cpu_baseline(d, abytes, args.cpu_rows, args.cpu_reps)
         log(f"cpu baseline {cpu} ({time.time() - t:.1f}s)")
 
     rec = {

@@ -182,9 +182,8 @@ int bf16x_kplan_build(const uint32_t* tile_off, const uint32_t* tile_ent, int64_
  * [M, out_f] of y_dtype (BF16X_BF16 or BF16X_F32).  Requires in_f % 64 == 0
  * and in_f <= 65536.  The call needs a workspace of
  * bf16x_gemm_workspace(M, out_f, in_f) bytes (0 = none; 16-byte aligned):
- * fp32 partials when K is split for parallelism and, for M <= 64 with
- * in_f % 128 == 0, x rearranged in decode order; a smaller one returns
- * BF16X_ECAPACITY.  All pointers dev.
+ * the fp32 partial products when K is split over workgroups for
+ * parallelism; a smaller one returns BF16X_ECAPACITY.  All pointers dev.
  * ------------------------------------------------------------------------ */
 int64_t bf16x_gemm_workspace(int64_t M, int64_t out_f, int64_t in_f);
 int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M,
