@@ -88,7 +88,7 @@ def time_launches(fn, n_launch: int, warmup: int, stream, queued: bool = False) 
 def cpu_baseline(d: dict, alg_bytes_full: int, rows: int, reps: int) -> dict:
     """The reference's CPU decode+matmul path (restated in oracle/cpu_path.py)
     on the first `rows` rows, median of `reps` timed passes after one warm-up
-    (about 13 s of CPU work at the defaults), scaled to compressed GB/s."""
+    (13-20 s of CPU work at the defaults), scaled to compressed GB/s."""
     from oracle.cpu_path import CpuBf16xLinear
     torch.set_num_threads(os.cpu_count() or 1)
     lin = CpuBf16xLinear(d, tile=1024)
@@ -349,7 +349,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=14336)
-    ap.add_argument("--cpu-reps", type=int, default=9)
+    ap.add_argument("--cpu-reps", type=int, default=15)
     ap.add_argument("--no-gguf", action="store_true", help="skip the GGUF (configuration 5) lines")
     ap.add_argument("--no-llama", action="store_true", help="skip the Llama-stack (configuration 4) line")
     ap.add_argument("--no-sweep", action="store_true",
