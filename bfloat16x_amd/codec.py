@@ -195,15 +195,23 @@ def build_plan_from_csr(olk, old, oloff, sign, mant, emax, out_f: int, in_f: int
     """Plan from the reference's device CSR (bf16x_fused.py:165-179): the
     offsets are reused as tile offsets, entries are re-encoded on the GPU."""
     dev = sign.device
+    for t, nm in ((olk, "olk"), (old, "old"), (oloff, "oloff")):
+        if not isinstance(t, torch.Tensor) or not t.is_cuda or t.device != dev or t.dtype != torch.int32:
+            raise ValueError(f"{nm} must be an int32 tensor on the streams' GPU ({dev})")
+    if oloff.numel() != int(out_f) + 1 or old.numel() != olk.numel():
+        raise ValueError("CSR shape: oloff needs out_f + 1 offsets and old one value per olk column")
+    olk, old, oloff = olk.contiguous(), old.contiguous(), oloff.contiguous()
     n = int(olk.numel())
     ent = torch.zeros(max(n, 1), dtype=torch.int32, device=dev)
     sat = torch.zeros(max(n, 1), dtype=torch.uint8, device=dev)
-    st = _lib.lib().bf16x_plan_from_csr(_lib.ptr(olk.contiguous()), _lib.ptr(old.contiguous()),
+    st = _lib.lib().bf16x_plan_from_csr(_lib.ptr(olk), _lib.ptr(old),
                                         oloff.data_ptr(), sign.data_ptr(), mant.data_ptr(), emax.data_ptr(),
                                         int(out_f), int(in_f), n, ent.data_ptr(), sat.data_ptr(),
                                         _lib.stream_of(dev))
     _lib.check(st, "bf16x_plan_from_csr")
-    return Bf16xPlan(oloff.to(torch.int32), ent, sat, n, int(out_f), int(in_f))
+    # the kernels read entries [off[r], off[r + 1]) of a row: offsets held in
+    # [0, n] keep every read inside the entry arrays whatever the caller's CSR
+    return Bf16xPlan(oloff.clamp(0, n), ent, sat, n, int(out_f), int(in_f))
 
 
 def build_plan_device(ovf_idx, ovf_val, sign, mant, emax, out_f: int, in_f: int) -> Bf16xPlan:

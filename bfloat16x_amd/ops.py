@@ -43,6 +43,33 @@ def _streams(sign, mant, delta, emax):
     return s, m, d, e
 
 
+def _on(t: torch.Tensor, dev: torch.device, name: str) -> torch.Tensor:
+    """t, required to live on the streams' GPU (kernels get raw pointers)."""
+    if not t.is_cuda or t.device != dev:
+        raise ValueError(f"{name} is on {t.device}, the weight streams on {dev}")
+    return t
+
+
+def _out(out, n: int, dev: torch.device, name: str = "out") -> torch.Tensor:
+    """A caller-supplied bf16 output: contiguous, on the streams' GPU, at least
+    n elements (the kernels write n elements through its pointer)."""
+    if not isinstance(out, torch.Tensor) or out.dtype != torch.bfloat16 or not out.is_contiguous() \
+            or out.numel() < n:
+        raise ValueError(f"{name} must be a contiguous bf16 tensor of at least {n} elements")
+    return _on(out, dev, name)
+
+
+def _plan_on(plan: Bf16xPlan | None, dev: torch.device, out_f: int, in_f: int) -> Bf16xPlan | None:
+    """A plan for this weight's shape on the streams' GPU (the kernels index
+    its offsets by row and column)."""
+    if plan is not None:
+        if (plan.out_f, plan.in_f) != (out_f, in_f):
+            raise ValueError(f"plan is for a {plan.out_f}x{plan.in_f} weight, not {out_f}x{in_f}")
+        for nm in ("tile_off", "tile_ent", "tile_sat"):
+            _on(getattr(plan, nm), dev, f"plan.{nm}")
+    return plan
+
+
 class _PlanCache:
     """Plans keyed by the identity and version of the tensors they came from.
     Entries hold references to those tensors, so a key cannot be reused by a
@@ -102,11 +129,12 @@ def bf16x_decode(sign, mant, delta, emax, out_f, in_f, ovf_idx=None, ovf_val=Non
     out_f, in_f = int(out_f), int(in_f)
     if plan is None and ovf_idx is not None and ovf_val is not None and ovf_val.numel() > 0:
         plan = plan_for_table(s, m, e, ovf_idx, ovf_val, out_f, in_f)
+    _plan_on(plan, s.device, out_f, in_f)
     mode = _lib.SATURATED if plan is None else _lib.EXACT
     if out is None:
         out = torch.empty(out_f, in_f, dtype=torch.bfloat16, device=s.device)
-    elif out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() != out_f * in_f:
-        raise ValueError("out must be a contiguous bf16 tensor of out_f*in_f elements")
+    else:
+        _out(out, out_f * in_f, s.device)
     st = _lib.lib().bf16x_decode(s.data_ptr(), s.numel(), m.data_ptr(), m.numel(), d.data_ptr(), d.numel(),
                                  e.data_ptr(), e.numel(), _lib.ptr(plan.tile_off) if plan else None,
                                  _lib.ptr(plan.tile_ent) if plan else None, out_f, in_f, int(sub), mode,
@@ -127,7 +155,9 @@ def bf16x_gemv(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None =
     out_f, in_f = int(out_f), int(in_f)
     if xx.numel() != in_f:
         raise ValueError(f"x has {xx.numel()} elements, in_f = {in_f}")
-    y = out if out is not None else torch.empty(out_f, dtype=torch.bfloat16, device=s.device)
+    _on(xx, s.device, "x")
+    _plan_on(plan, s.device, out_f, in_f)
+    y = _out(out, out_f, s.device) if out is not None else torch.empty(out_f, dtype=torch.bfloat16, device=s.device)
     mode = _lib.SATURATED if plan is None else _lib.EXACT
     st = _lib.lib().bf16x_gemv(xx.data_ptr(), _X_DTYPES[xx.dtype], s.data_ptr(), s.numel(), m.data_ptr(),
                                m.numel(), d.data_ptr(), d.numel(), e.data_ptr(), e.numel(),
@@ -147,9 +177,10 @@ def bf16x_gemv_swiglu(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan |
     out_f, in_f = int(out_f), int(in_f)
     if xx.numel() != in_f:
         raise ValueError(f"x has {xx.numel()} elements, in_f = {in_f}")
-    y = out if out is not None else torch.empty(out_f // 2, dtype=torch.bfloat16, device=s.device)
-    if y.dtype != torch.bfloat16 or not y.is_contiguous() or y.numel() < out_f // 2:
-        raise ValueError("out must be a contiguous bf16 tensor of out_f / 2 elements")
+    _on(xx, s.device, "x")
+    _plan_on(plan, s.device, out_f, in_f)
+    y = _out(out, out_f // 2, s.device) if out is not None else \
+        torch.empty(out_f // 2, dtype=torch.bfloat16, device=s.device)
     mode = _lib.SATURATED if plan is None else _lib.EXACT
     st = _lib.lib().bf16x_gemv_swiglu(xx.data_ptr(), s.data_ptr(), s.numel(), m.data_ptr(), m.numel(), d.data_ptr(),
                                       d.numel(), e.data_ptr(), e.numel(),
@@ -173,16 +204,16 @@ def bf16x_gemv_norm(x, residual_in, norm_weight, residual_out, eps, sign, mant, 
     xx = _dev_tensor(x, "x", bf).reshape(-1)
     nw = _dev_tensor(norm_weight, "norm_weight", bf).reshape(-1)
     ri = _dev_tensor(residual_in, "residual_in", bf).reshape(-1) if residual_in is not None else None
-    if residual_out is not None and (not residual_out.is_cuda or residual_out.dtype != torch.bfloat16
-                                     or not residual_out.is_contiguous() or residual_out.numel() < in_f):
-        raise ValueError("residual_out must be a contiguous bf16 GPU tensor of in_f elements")
+    if residual_out is not None:
+        _out(residual_out, in_f, s.device, "residual_out")
     for t, nm in ((xx, "x"), (nw, "norm_weight"), (ri, "residual_in")):
-        if t is not None and t.numel() != in_f:
-            raise ValueError(f"{nm} has {t.numel()} elements, in_f = {in_f}")
+        if t is not None:
+            _on(t, s.device, nm)
+            if t.numel() != in_f:
+                raise ValueError(f"{nm} has {t.numel()} elements, in_f = {in_f}")
+    _plan_on(plan, s.device, out_f, in_f)
     n_out = out_f // 2 if swiglu else out_f
-    y = out if out is not None else torch.empty(n_out, dtype=torch.bfloat16, device=s.device)
-    if y.dtype != torch.bfloat16 or not y.is_contiguous() or y.numel() < n_out:
-        raise ValueError("out must be a contiguous bf16 tensor of the output length")
+    y = _out(out, n_out, s.device) if out is not None else torch.empty(n_out, dtype=torch.bfloat16, device=s.device)
     mode = _lib.SATURATED if plan is None else _lib.EXACT
     st = _lib.lib().bf16x_gemv_norm(xx.data_ptr(), _lib.ptr(ri), nw.data_ptr(), _lib.ptr(residual_out), float(eps),
                                     s.data_ptr(), s.numel(), m.data_ptr(), m.numel(), d.data_ptr(), d.numel(),
@@ -249,9 +280,10 @@ def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None =
         raise ValueError(f"path must be auto, fused or decode, not {path!r}")
     s, m, d, e = _streams(sign, mant, delta, emax)
     out_f, in_f = int(out_f), int(in_f)
-    xx = _dev_tensor(x, "x", tuple(_X_DTYPES))
+    xx = _on(_dev_tensor(x, "x", tuple(_X_DTYPES)), s.device, "x")
     if xx.shape[-1] != in_f:
         raise ValueError(f"x has last dimension {xx.shape[-1]}, in_f = {in_f}")
+    _plan_on(plan, s.device, out_f, in_f)
     lead = xx.shape[:-1]
     x2 = xx.reshape(-1, in_f)
     if x2.shape[0] == 0:

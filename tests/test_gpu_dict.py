@@ -139,6 +139,64 @@ def test_fused_gemv_reference_csr(bx):
     check_tol(y.float().cpu().numpy(), y_ref)
 
 
+def test_ops_reject_mismatched_buffers(bx):
+    """The wrappers hand raw pointers to the kernels, so every caller-supplied
+    buffer is checked first: an output too small or on the CPU, a plan built
+    for another shape, a reference CSR of the wrong dtype or length.  Each is
+    refused on the host before any launch."""
+    shape = (256, 1024)
+    bits = dc.bench_weight_bits(*shape, seed=21)
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    streams = (g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"])
+    plan = bx.build_plan_host(d, device=DEV)
+    x = torch.randn(shape[1], generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(DEV)
+    with pytest.raises(ValueError):
+        bx.bf16x_gemv(x, *streams, *shape, plan=plan, out=torch.empty(shape[0] - 1, dtype=torch.bfloat16,
+                                                                       device=DEV))
+    with pytest.raises(ValueError):
+        bx.bf16x_gemv(x, *streams, *shape, plan=plan, out=torch.empty(shape[0], dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        bx.bf16x_decode(*streams, *shape, plan=plan, out=torch.empty(shape[0] * shape[1], dtype=torch.bfloat16))
+    other = bx.build_plan_host(bx.bf16x_quantize(bits_tensor(dc.bench_weight_bits(128, 1024, seed=3))), device=DEV)
+    for call in (lambda: bx.bf16x_gemv(x, *streams, *shape, plan=other),
+                 lambda: bx.bf16x_decode(*streams, *shape, plan=other),
+                 lambda: bx.bf16x_gemm(x.reshape(1, -1).repeat(80, 1), *streams, *shape, plan=other)):
+        with pytest.raises(ValueError):
+            call()
+    k = torch.zeros(4, dtype=torch.int64, device=DEV)
+    v = torch.full((4,), 9, dtype=torch.int32, device=DEV)
+    off = torch.zeros(shape[0] + 1, dtype=torch.int32, device=DEV)
+    with pytest.raises(ValueError):
+        bx.bf16x_fused_gemv(x, *streams, k, v, off, *shape)               # int64 columns
+    with pytest.raises(ValueError):
+        bx.bf16x_fused_gemv(x, *streams, k.to(torch.int32), v, off[:-1], *shape)   # short offsets
+    # the calls that pass still agree with the oracle
+    y = bx.bf16x_gemv(x, *streams, *shape, plan=plan, out=torch.empty(shape[0], dtype=torch.bfloat16, device=DEV))
+    check_tol(y.float().cpu().numpy(), dc.bits_to_f32(bits).astype(np.float64) @ x.float().cpu().numpy())
+
+
+def test_fused_gemv_csr_offsets_are_clamped(bx):
+    """A reference CSR whose offsets point past its entries (a malformed
+    table) cannot make a kernel read outside the entry arrays: the plan keeps
+    the offsets in [0, n], and the rows whose runs were cut lose only their
+    corrections."""
+    shape = (64, 1024)
+    bits = dc.bench_weight_bits(*shape, seed=22)
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    x = torch.randn(shape[1], generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(DEV)
+    k = torch.tensor([3, 7], dtype=torch.int32, device=DEV)
+    v = torch.tensor([9, 10], dtype=torch.int32, device=DEV)
+    off = torch.full((shape[0] + 1,), 2, dtype=torch.int32, device=DEV)
+    off[0] = 0
+    off[-1] = 1 << 20                                                    # past the two entries
+    plan = bx.ops.plan_for_csr(k, v, off, g["sign_packed"], g["mant_packed"], g["emax"], *shape)
+    assert int(plan.tile_off.max()) == 2
+    y = bx.bf16x_gemv(x, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], *shape, plan=plan)
+    assert torch.isfinite(y.float()).all()
+
+
 def test_full_size_roundtrip_and_gemv(bx):
     """14336x4096 at full size: encode -> exact decode is the identity on the
     original bits, and the GEMV matches fp32 matmul of the decoded weight."""
