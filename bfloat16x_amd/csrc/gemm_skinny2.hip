@@ -378,18 +378,24 @@ struct Split {
 };
 
 // Token blocks of 16 and waves per row group for M activation rows: KQ = 4
-// up to 32 rows (16 waves per workgroup), 1 above (the x tile of 4 steps for
-// 64 tokens would not fit beside the scratch).
+// up to 32 rows (16 waves per workgroup), 2 above (8 waves: the x tile of 4
+// steps for 64 tokens would not fit beside the scratch, the tile of 2 steps
+// does; 64 rows at 14336 x 4096: 47 us against 55 us with one wave per
+// row group).  BF16X_SKINNY2_KQ=1 or 2 overrides.
 int nc_for(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
 int kq_for(int64_t M) {
-  if (const char* e = getenv("BF16X_SKINNY2_KQ")) return atoi(e) == 1 ? 1 : (nc_for(M) <= 2 ? 4 : 1);
-  return nc_for(M) <= 2 ? 4 : 1;
+  if (const char* e = getenv("BF16X_SKINNY2_KQ")) {
+    const int k = atoi(e);
+    if (k == 1) return 1;
+    if (k == 2) return 2;
+  }
+  return nc_for(M) <= 2 ? 4 : 2;
 }
 
 // Workgroups of the (NC, KQ, EXACT) kernel resident at once on the current
 // device, from the runtime's occupancy calculation (registers and LDS of the
-// compiled kernel); 3 (KQ = 1) or 1 (KQ = 4) per CU on 256 CUs when there is
-// no device to ask.
+// compiled kernel); 3 (KQ = 1) or 1 (KQ = 2, 4) per CU on 256 CUs when there
+// is no device to ask.
 template <int NC, int KQ, bool EXACT>
 int64_t resident_slots() {
   static int64_t cache[64];
@@ -411,6 +417,11 @@ int64_t slots_for(int64_t M, bool exact) {
   if (kq == 4) {
     if (nc == 1) return exact ? resident_slots<1, 4, true>() : resident_slots<1, 4, false>();
     return exact ? resident_slots<2, 4, true>() : resident_slots<2, 4, false>();
+  }
+  if (kq == 2) {
+    if (nc == 4) return exact ? resident_slots<4, 2, true>() : resident_slots<4, 2, false>();
+    if (nc == 2) return exact ? resident_slots<2, 2, true>() : resident_slots<2, 2, false>();
+    return exact ? resident_slots<1, 2, true>() : resident_slots<1, 2, false>();
   }
   if (nc == 1) return exact ? resident_slots<1, 1, true>() : resident_slots<1, 1, false>();
   if (nc == 2) return exact ? resident_slots<2, 1, true>() : resident_slots<2, 1, false>();
@@ -485,6 +496,10 @@ int bf16x_gemm_skinny2_launch(const uint16_t* x, int64_t M, const uint32_t* s, c
   if (kq == 4) {
     if (nc == 1) BF16X_S2_NC(1, 4);
     else BF16X_S2_NC(2, 4);
+  } else if (kq == 2) {
+    if (nc == 1) BF16X_S2_NC(1, 2);
+    else if (nc == 2) BF16X_S2_NC(2, 2);
+    else BF16X_S2_NC(4, 2);
   } else {
     switch (nc) {
       case 1: BF16X_S2_NC(1, 1); break;

@@ -512,12 +512,13 @@ int launch_gemv(const void* x, const uint32_t* sign, const uint32_t* mant, const
     const bool full = (XT == BF16X_BF16) && P == (int64_t)G * 64 * NS;
     const int rpi = 4 / G;
     const int64_t groups = (out_f + rpi - 1) / rpi;
-    // Row groups per workgroup (measured at the configuration-2 shapes): 2
-    // from 2048 groups on; 4 for rows split over 4 waves (long rows), where
-    // the 4096 x 14336 grid then fits one round of resident workgroups
-    // (21.6 us against 23.0 us with 2).
+    // Row groups per workgroup (measured at the configuration-2 and -4
+    // shapes): 2 from 1024 groups on (6144 x 4096: 10.6 us against 11.7 us
+    // with 1; 4096 x 4096: 8.2 against 8.5); 4 for rows split over 4 waves
+    // (long rows) from 2048 groups on, where the 4096 x 14336 grid then fits
+    // one round of resident workgroups (21.6 us against 23.0 us with 2).
     int iters = gemv_iters_override();
-    if (iters <= 0) iters = groups >= 2048 ? (G == 4 ? 4 : 2) : 1;
+    if (iters <= 0) iters = groups >= 2048 ? (G == 4 ? 4 : 2) : (groups >= 1024 ? 2 : 1);
     const int64_t grid = (groups + iters - 1) / iters;
     if (grid > INT32_MAX) return BF16X_ESHAPE;
 #define BF16X_PIPE1(NS_, G_, EX_, FULL_)                                                             \

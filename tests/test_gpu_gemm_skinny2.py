@@ -64,6 +64,22 @@ def test_skinny2_fp32_product(bx, M, out_f, in_f):
         assert mx <= 1e-3 and med <= 1e-6, (sat, mx, med)
 
 
+@pytest.mark.parametrize("kq", ["1", "2"])
+@pytest.mark.parametrize("M,out_f,in_f", [(5, 130, 4096), (33, 72, 1024), (48, 384, 14336), (64, 200, 2048)])
+def test_skinny2_waves_per_row_group(bx, monkeypatch, kq, M, out_f, in_f):
+    """The other wave-per-row-group counts (BF16X_SKINNY2_KQ=1: one wave walks
+    every step of its rows; 2: two waves take alternate steps) give the same
+    fp32 product: the default is 4 up to 32 rows and 2 above."""
+    monkeypatch.setenv("BF16X_SKINNY2_KQ", kq)
+    bits, d, g, plan = _weight(bx, out_f, in_f, seed=M + out_f + 7)
+    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M + 1)).to(torch.bfloat16).float()
+    dn = _np(d)
+    for p, sat in ((plan, False), (None, True)):
+        y = _gemm(bx, x.to(DEV), g, out_f, in_f, p)
+        mx, med = dc.rel_err(y.cpu().numpy(), dc.gemm_ref(dn, x.double().numpy(), saturated=sat))
+        assert mx <= 1e-3 and med <= 1e-6, (kq, sat, mx, med)
+
+
 @pytest.mark.parametrize("M", [1, 16, 40, 64])
 def test_skinny2_identity_is_bit_exact(bx, M):
     out_f, in_f = 136, 512
