@@ -434,6 +434,190 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
   }
 }
 
+// Long rows (in_f > 4096, bf16 x): one wave per row, the row streamed in NP
+// passes of 64 atoms (lane l takes atom 64c + l of pass c) through a
+// two-slot register ring that runs on across the wave's rows, so the next
+// row's first atoms are in flight while a row's last pass is decoded.  x is
+// staged once per workgroup in LDS (the pipelined kernel's lane-major
+// layout); the workgroup's 4 waves take rows base + 4i + wave, i < iters.
+// No cross-wave reduction and no barrier in the main loop (the split-K
+// kernel above exchanges partial sums through LDS once per row).  Plan
+// offsets are read two rows ahead and the first NB * 64 entries of a row one
+// row ahead; a row with more entries (rare) parks its fp32 sum in LDS and
+// gets its remaining entries after the last row (a loop inside the row loop
+// would make the compiler keep the whole pass schedule's registers live).
+constexpr int kLongMaxIters = 16;
+
+template <int NP, int XS, bool EXACT, bool FULL>
+__global__ __launch_bounds__(256) void gemv_long_kernel(
+    const uint16_t* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
+    const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
+    const uint32_t* __restrict__ tile_off, const uint32_t* __restrict__ tile_ent,
+    const uint8_t* __restrict__ tile_sat, int64_t out_f, int64_t in_f, int iters, uint16_t* __restrict__ y) {
+  static_assert(NP >= 2, "at least two passes per row");
+  constexpr int NB = 6;                         // entry batches of 64 read ahead per row
+  extern __shared__ uint32_t lds[];
+  __shared__ float dpart[4][kLongMaxIters];     // parked rows: fp32 sum and row index i
+  __shared__ int drow[4][kLongMaxIters];
+  // uniform: the row enters the loads as a scalar offset
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t P = in_f >> 5;
+
+  const __amdgpu_buffer_rsrc_t rs_ = buf_rsrc(sign, (uint64_t)out_f * P * 4);
+  const __amdgpu_buffer_rsrc_t rm_ = buf_rsrc(mant, (uint64_t)out_f * P * 28);
+  const __amdgpu_buffer_rsrc_t rd_ = buf_rsrc(delta, (uint64_t)out_f * P * 12);
+  const __amdgpu_buffer_rsrc_t re_ = buf_rsrc(emax2, (uint64_t)out_f * P * 2);
+  const __amdgpu_buffer_rsrc_t roff = buf_rsrc(tile_off, (uint64_t)(out_f + 1) * 4);
+  const __amdgpu_buffer_rsrc_t rent = buf_rsrc(tile_ent, 0xFFFFFFFFull);   // reads clamped into the row
+  const __amdgpu_buffer_rsrc_t rsat = buf_rsrc(tile_sat, 0xFFFFFFFFull);
+
+  // XCD-aware order, as in the pipelined kernel
+  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
+  const int per = nb / 8, extra = nb - per * 8;
+  const int lb = nb >= 8 ? ((b & 7) * per + min(b & 7, extra) + (b >> 3)) : b;
+  const int64_t base = (int64_t)lb * iters * 4 + wave;
+  auto row_of = [&](int i) { return min(base + 4 * (int64_t)min(i, iters - 1), out_f - 1); };
+  auto load_pass = [&](int i, int c, Atom& t) {
+    const uint32_t sa = (uint32_t)(row_of(i) * P);
+    const uint32_t va = (uint32_t)min((int64_t)(64 * c + lane), P - 1);
+    t = load_atom_buf(rs_, rm_, rd_, re_, va, sa);
+  };
+  auto load_off = [&](int i, uint32_t& b0, uint32_t& b1) {
+    const int rc = (int)row_of(i);
+    b0 = __builtin_amdgcn_raw_buffer_load_b32(roff, rc * 4, 0, 0);
+    b1 = __builtin_amdgcn_raw_buffer_load_b32(roff, rc * 4 + 4, 0, 0);
+  };
+  auto load_ents = [&](uint32_t b0, uint32_t b1, uint32_t* ent, uint8_t* sat) {
+    const uint32_t last = b1 > 0 ? b1 - 1 : 0;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const uint32_t e = min(b0 + (uint32_t)(lane + 64 * k), last);
+      ent[k] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)(e * 4), 0, 0);
+      sat[k] = __builtin_amdgcn_raw_buffer_load_b8(rsat, (int)e, 0, 0);
+    }
+  };
+  auto x_at = [&](uint32_t k) -> float {
+    const uint32_t a = k >> 5, j = k & 15, hi = (k >> 4) & 1;
+    const uint32_t wd = lds[((((a >> 6) * 4) + (j >> 2)) * 64 + (a & 63)) * 4 + (j & 3)];
+    return hi ? bf16hi_to_f32(wd) : bf16lo_to_f32(wd);
+  };
+
+  // prologue, in the order the data is needed: offsets of rows 0 and 1, x
+  // (registers), the first two passes, the entries of row 0; x to LDS
+  uint32_t ob0 = 0, ob1 = 0, on0 = 0, on1 = 0;
+  if constexpr (EXACT) {
+    load_off(0, ob0, ob1);
+    load_off(1, on0, on1);
+  }
+  uint32_t xs[XS][16];
+#pragma unroll
+  for (int i = 0; i < XS; ++i) load_x_atom<BF16X_BF16>(x, min((int64_t)(threadIdx.x + 256 * i), P - 1), xs[i]);
+  Atom R[2];
+  load_pass(0, 0, R[0]);
+  load_pass(0, 1, R[1]);
+  uint32_t ent[NB] = {};
+  uint8_t sat[NB] = {};
+  if constexpr (EXACT) load_ents(ob0, ob1, ent, sat);
+#pragma unroll
+  for (int i = 0; i < XS; ++i) {
+    const int a = threadIdx.x + 256 * i;
+    if (a < NP * 64) {
+      u32x4* dst = (u32x4*)lds + (a >> 6) * 4 * 64 + (a & 63);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dst[c * 64] = u32x4{xs[i][4 * c], xs[i][4 * c + 1], xs[i][4 * c + 2], xs[i][4 * c + 3]};
+    }
+  }
+  __syncthreads();
+
+  const u32x4* xl = (const u32x4*)lds + lane;
+  float acc0 = 0.f, acc1 = 0.f;
+  bool more = false;                            // uniform: the row has entries past the batches
+  int nparked = 0;                              // uniform
+  // row i; its pass c sits in ring slot (PAR + c) % 2 and is refilled with
+  // the pass two ahead (in this row or the next) once decoded
+  auto do_row = [&](int i, auto par) {
+    constexpr int PAR = decltype(par)::value;
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+      Atom& cur = R[(PAR + c) & 1];
+      uint32_t xr[16];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 v = xl[(c * 4 + q) * 64];
+        xr[4 * q] = v.x; xr[4 * q + 1] = v.y; xr[4 * q + 2] = v.z; xr[4 * q + 3] = v.w;
+      }
+      if (FULL || c < NP - 1) {
+        dot_atom<BF16X_BF16>(cur, xr, acc0, acc1);
+      } else {
+        float t0 = 0.f, t1 = 0.f;
+        dot_atom<BF16X_BF16>(cur, xr, t0, t1);
+        const bool live = (int64_t)(64 * c + lane) < P;
+        acc0 += live ? t0 : 0.f;
+        acc1 += live ? t1 : 0.f;
+      }
+      if (c + 2 < NP) load_pass(i, c + 2, cur);
+      else load_pass(i + 1, c + 2 - NP, cur);
+      // keep each refill right behind its decode (the issue order is the
+      // consumption order)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (EXACT) {
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        const uint32_t e = ob0 + (uint32_t)(lane + 64 * k);
+        const uint32_t kk = min(ent[k] >> 16, (uint32_t)in_f - 1);
+        const uint32_t sbits = (ent[k] & 0x807Fu) | ((uint32_t)sat[k] << 7);
+        const float cc = (bf16lo_to_f32(ent[k]) - bf16lo_to_f32(sbits)) * x_at(kk);
+        acc0 += (e < ob1) ? cc : 0.f;
+      }
+      more = __builtin_amdgcn_readfirstlane(ob1) > __builtin_amdgcn_readfirstlane(ob0) + 64u * NB;
+      uint32_t nn0, nn1;
+      load_off(i + 2, nn0, nn1);
+      load_ents(on0, on1, ent, sat);
+      ob0 = on0; ob1 = on1; on0 = nn0; on1 = nn1;
+    }
+    const float tot = wave_sum_dpp(acc0 + acc1);
+    const int64_t r = base + 4 * (int64_t)i;
+    if (EXACT && more) {                        // finished after the last row
+      if (lane == 63) {
+        dpart[wave][nparked] = tot;
+        drow[wave][nparked] = i;
+      }
+      ++nparked;
+    } else if (lane == 63 && r < out_f) {
+      y[r] = (uint16_t)f32_to_bf16_rne(tot);
+    }
+    acc0 = 0.f;
+    acc1 = 0.f;
+  };
+  if constexpr (NP % 2 == 0) {
+    for (int i = 0; i < iters; ++i) do_row(i, std::integral_constant<int, 0>{});
+  } else {
+    int i = 0;
+    for (; i + 1 < iters; i += 2) {
+      do_row(i, std::integral_constant<int, 0>{});
+      do_row(i + 1, std::integral_constant<int, 1>{});
+    }
+    if (i < iters) do_row(i, std::integral_constant<int, 0>{});
+  }
+  // parked rows: entries past the read-ahead batches (same wave's LDS
+  // writes, read back in issue order)
+  for (int d = 0; d < nparked; ++d) {
+    const int i = __builtin_amdgcn_readfirstlane(drow[wave][d]);
+    const int64_t r = base + 4 * (int64_t)i;
+    const uint32_t b0 = tile_off[row_of(i)], b1 = tile_off[row_of(i) + 1];
+    float a = 0.f;
+    for (uint32_t e = b0 + 64u * NB + (uint32_t)lane; e < b1; e += 64) {
+      const uint32_t en = tile_ent[e];
+      const uint32_t kk = min(en >> 16, (uint32_t)in_f - 1);
+      const uint32_t sbits = (en & 0x807Fu) | ((uint32_t)tile_sat[e] << 7);
+      a = fmaf(bf16lo_to_f32(en) - bf16lo_to_f32(sbits), x_at(kk), a);
+    }
+    const float tot = wave_sum_dpp(a) + dpart[wave][d];
+    if (lane == 63 && r < out_f) y[r] = (uint16_t)f32_to_bf16_rne(tot);
+  }
+}
+
 // Any in_f % 32 == 0 (e.g. beyond the pipelined kernel's 16384 columns):
 // one wave per row, x values read from global memory per atom.
 template <int XT>
@@ -489,12 +673,55 @@ int gemv_g_override() {
   return v;
 }
 
+// BF16X_GEMV_LONG=0 sends long rows to the split-K kernel instead.
+bool gemv_long_enabled() {
+  static bool v = getenv("BF16X_GEMV_LONG") == nullptr || env_int("BF16X_GEMV_LONG") != 0;
+  return v;
+}
+
+// Long rows (bf16 x, 4096 < in_f <= 16384): the one-wave-per-row kernel
+// (4096 x 14336 exact: 20.5 us against 22.4 us for the split-K kernel;
+// 2048 x 14336: 11.5 against 13.3).
+int launch_gemv_long(const void* x, const uint32_t* sign, const uint32_t* mant, const uint32_t* delta,
+                     const uint16_t* emax2, const uint32_t* to, const uint32_t* te, const uint8_t* ts,
+                     int64_t out_f, int64_t in_f, uint16_t* y, hipStream_t st) {
+  const int64_t P = in_f >> 5;
+  const int np = (int)((P + 63) / 64);
+  const bool full = P % 64 == 0;
+  const size_t lds = (size_t)np * 4 * 64 * 16;
+  const int64_t groups = (out_f + 3) / 4;
+  // rows per wave (measured): 4 from 2048 groups of 4 rows, 2 from 1024
+  int iters = gemv_iters_override();
+  if (iters <= 0) iters = groups >= 2048 ? 4 : (groups >= 1024 ? 2 : 1);
+  iters = std::min(iters, kLongMaxIters);
+  const int64_t grid = (groups + iters - 1) / iters;
+  if (grid > INT32_MAX) return BF16X_ESHAPE;
+#define BF16X_LONG1(NP_, EX_, FU_)                                                                              \
+  hipLaunchKernelGGL((gemv_long_kernel<NP_, 2, EX_, FU_>), dim3((unsigned)grid), dim3(256), lds, st,             \
+                     (const uint16_t*)x, sign, mant, delta, emax2, to, te, ts, out_f, in_f, iters, y)
+#define BF16X_LONG(NP_)                                                                                        \
+  case NP_:                                                                                                    \
+    if (to) { if (full) BF16X_LONG1(NP_, true, true); else BF16X_LONG1(NP_, true, false); }                    \
+    else { if (full) BF16X_LONG1(NP_, false, true); else BF16X_LONG1(NP_, false, false); }                     \
+    break;
+  switch (np) {
+    BF16X_LONG(3) BF16X_LONG(4) BF16X_LONG(5) BF16X_LONG(6) BF16X_LONG(7) BF16X_LONG(8)
+    default: return BF16X_ESHAPE;
+  }
+#undef BF16X_LONG
+#undef BF16X_LONG1
+  return launch_status();
+}
+
 template <int XT>
 int launch_gemv(const void* x, const uint32_t* sign, const uint32_t* mant, const uint32_t* delta,
                 const uint16_t* emax2, const uint32_t* to, const uint32_t* te, const uint8_t* ts, int64_t out_f,
                 int64_t in_f, uint16_t* y, hipStream_t st) {
   const int64_t P = in_f >> 5;
   const int tpr = tiles_per_row(in_f);
+  if (XT == BF16X_BF16 && gemv_long_enabled() && P > 128 && P <= 512 && tpr == 1 &&
+      (out_f + 1) * P * 28 < (int64_t)0xFFFFFFFF)
+    return launch_gemv_long(x, sign, mant, delta, emax2, to, te, ts, out_f, in_f, y, st);
   // parts of 64*NS atoms per wave; G = ceil(P / (64*NS)) waves per row.
   // NS = 2 unless rows are few (then 1, for more waves in flight).
   int NS = (P > 64) ? 2 : 1;

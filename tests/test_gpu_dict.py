@@ -197,6 +197,33 @@ def test_fused_gemv_csr_offsets_are_clamped(bx):
     assert torch.isfinite(y.float()).all()
 
 
+@pytest.mark.parametrize("out_f,in_f", [(4100, 6144), (40, 4128), (1030, 16384)])
+def test_gemv_long_rows_dense_overflow(bx, out_f, in_f):
+    """Rows longer than 4096 columns (the one-wave-per-row kernel) with far
+    more plan entries than the batches read ahead per row: 30 % of the
+    elements are tiny (delta >= 7 next to normal values), so every row parks
+    its sum and finishes its entries after the wave's last row; ragged row
+    counts, a partial last pass (4128 columns), one and two rows per wave."""
+    bits = dc.bench_weight_bits(out_f, in_f, seed=in_f)
+    rng = np.random.default_rng(in_f)
+    tiny = rng.random(bits.shape) < 0.3
+    bits[tiny] = (bits[tiny] & 0x807F) | 0x0080
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    plan = bx.build_plan_host(d, device=DEV)
+    assert plan.n_fix > out_f * 6 * 64
+    g = to_dev(d)
+    x = torch.randn(in_f, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+    y = bx.bf16x_gemv(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                      plan=plan)
+    y_ref = dc.bits_to_f32(bits).astype(np.float64) @ x.float().numpy().astype(np.float64)
+    check_tol(y.float().cpu().numpy(), y_ref)
+    ys = bx.bf16x_gemv(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f)
+    ys_ref = dc.bits_to_f32(dc.decode_saturated({k: (v.numpy() if isinstance(v, torch.Tensor) else v)
+                                                 for k, v in d.items()})).astype(np.float64) @ \
+        x.float().numpy().astype(np.float64)
+    check_tol(ys.float().cpu().numpy(), ys_ref)
+
+
 def test_full_size_roundtrip_and_gemv(bx):
     """14336x4096 at full size: encode -> exact decode is the identity on the
     original bits, and the GEMV matches fp32 matmul of the decoded weight."""
