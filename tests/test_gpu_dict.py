@@ -210,7 +210,7 @@ def test_gemv_long_rows_dense_overflow(bx, out_f, in_f):
     bits[tiny] = (bits[tiny] & 0x807F) | 0x0080
     d = bx.bf16x_quantize(bits_tensor(bits))
     plan = bx.build_plan_host(d, device=DEV)
-    assert plan.n_fix > out_f * 6 * 64
+    assert plan.n_fix > out_f * (in_f // 2048) * 64
     g = to_dev(d)
     x = torch.randn(in_f, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
     y = bx.bf16x_gemv(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
