@@ -234,6 +234,19 @@ __device__ __forceinline__ float dot2_bf16(uint32_t w, uint32_t x, float acc) {
   return __builtin_amdgcn_fdot2_f32_bf16(a, b, acc, false);
 }
 
+// Sum over the 64 lanes of a wave with DPP: row scans (shr 1, 2, 4, 8) leave
+// each 16-lane row's sum in its lane 15, row_bcast 15/31 fold the rows; the
+// total ends in lane 63.
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x111, 0xF, 0xF, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x112, 0xF, 0xF, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x114, 0xF, 0xF, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x118, 0xF, 0xF, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0.f, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);

@@ -112,19 +112,6 @@ __device__ __forceinline__ Atom load_atom_buf(__amdgpu_buffer_rsrc_t rs, __amdgp
   return t;
 }
 
-// Sum over the 64 lanes of a wave with DPP: row scans (shr 1, 2, 4, 8) leave
-// each 16-lane row's sum in its lane 15, row_bcast 15/31 fold the rows; the
-// total ends in lane 63.
-__device__ __forceinline__ float wave_sum_dpp(float v) {
-  v += __builtin_amdgcn_update_dpp(0.f, v, 0x111, 0xF, 0xF, false);  // row_shr:1
-  v += __builtin_amdgcn_update_dpp(0.f, v, 0x112, 0xF, 0xF, false);  // row_shr:2
-  v += __builtin_amdgcn_update_dpp(0.f, v, 0x114, 0xF, 0xF, false);  // row_shr:4
-  v += __builtin_amdgcn_update_dpp(0.f, v, 0x118, 0xF, 0xF, false);  // row_shr:8
-  v += __builtin_amdgcn_update_dpp(0.f, v, 0x142, 0xA, 0xF, false);  // row_bcast:15
-  v += __builtin_amdgcn_update_dpp(0.f, v, 0x143, 0xC, 0xF, false);  // row_bcast:31
-  return v;
-}
-
 // Pipelined decode+GEMV.
 //
 // Work split: a row's P atoms are cut into parts of 64*NS atoms (the last

@@ -9,6 +9,10 @@
 // serves both formats (decode_pairs<true>).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
+
+#include <algorithm>
+#include <type_traits>
 
 #include "../../include/bf16x_hip.h"
 #include "bf16x_device.h"
@@ -224,6 +228,181 @@ __global__ __launch_bounds__(256) void gguf_gemv_kernel(const uint8_t* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// GEMV for rows of 64k columns (k >= 3, in_f <= 32768): the dict GEMV's
+// long-row structure (gemv.hip, gemv_long_kernel).  One wave per row, the
+// row streamed in NP passes of 64 blocks through a two-slot register ring
+// that runs on across the wave's rows; paired x staged once per workgroup in
+// LDS (lane-major: chunk (4 pass + q) * 64 + lane holds pair words 4q .. 4q+3
+// of block 64 pass + lane); workgroup rows base + 4 i + wave, i < iters.  The
+// row's base byte offset is a multiple of 4 (P even), so it enters the loads
+// as a scalar offset and the 2-byte skew of a block is its lane's.  OVF: the
+// side-table entries of a row (first 64 NP read one row ahead, the rest after
+// the wave's last row), each adding (exact - marker) * x[col].
+constexpr int kLongMaxIters = 16;
+
+template <int NP, int XS, bool YF32, bool OVF>
+__global__ __launch_bounds__(256) void gguf_gemv_long_kernel(const uint8_t* __restrict__ blocks,
+                                                             const uint32_t* __restrict__ xp, int64_t out_f,
+                                                             int64_t in_f, const uint32_t* __restrict__ ovf_off,
+                                                             const uint32_t* __restrict__ ovf_ent, int iters,
+                                                             void* __restrict__ y) {
+  static_assert(NP >= 2, "at least two passes per row");
+  constexpr int NB = NP;
+  extern __shared__ uint32_t lds[];
+  __shared__ float dpart[4][kLongMaxIters];
+  __shared__ int drow[4][kLongMaxIters];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int64_t P = in_f >> 5;
+  const uint64_t total = ((uint64_t)out_f * P * kBlockBytes + 3) & ~3ull;
+  const __amdgpu_buffer_rsrc_t rs = rsrc(blocks, total);
+  const __amdgpu_buffer_rsrc_t roff = rsrc(ovf_off, OVF ? (uint64_t)(out_f + 1) * 4 : 0);
+
+  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
+  const int per = nb / 8, extra = nb - per * 8;
+  const int lb = nb >= 8 ? ((b & 7) * per + min(b & 7, extra) + (b >> 3)) : b;
+  const int64_t base = (int64_t)lb * iters * 4 + wave;
+  auto row_of = [&](int i) { return min(base + 4 * (int64_t)min(i, iters - 1), out_f - 1); };
+  auto load_pass = [&](int i, int c, GgufRaw& t) {
+    const uint32_t so = (uint32_t)(row_of(i) * P * kBlockBytes);   // multiple of 4
+    const uint32_t boff = (uint32_t)min((int64_t)(64 * c + lane), P - 1) * kBlockBytes;
+    const uint32_t vb = boff & ~3u;
+    t.sh = (boff & 2u) * 8u;
+    t.q0 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)vb, (int)so, 0);
+    t.q1 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(vb + 16), (int)so, 0);
+    t.q2 = __builtin_amdgcn_raw_buffer_load_b128(rs, (int)(vb + 32), (int)so, 0);
+  };
+  auto load_off = [&](int i, uint32_t& b0, uint32_t& b1) {
+    const int rc = (int)row_of(i);
+    b0 = __builtin_amdgcn_raw_buffer_load_b32(roff, rc * 4, 0, 0);
+    b1 = __builtin_amdgcn_raw_buffer_load_b32(roff, rc * 4 + 4, 0, 0);
+  };
+  auto load_ents = [&](uint32_t b0, uint32_t b1, uint32_t* ent) {
+    const uint32_t last = b1 > 0 ? b1 - 1 : 0;
+#pragma unroll
+    for (int k = 0; k < NB; ++k) ent[k] = ovf_ent[min(b0 + (uint32_t)(lane + 64 * k), last)];
+  };
+  auto x_at = [&](uint32_t k) -> float {
+    const uint32_t a = k >> 5, j = k & 15, hi = (k >> 4) & 1;
+    const uint32_t wd = lds[((((a >> 6) * 4) + (j >> 2)) * 64 + (a & 63)) * 4 + (j & 3)];
+    return hi ? bf16hi_to_f32(wd) : bf16lo_to_f32(wd);
+  };
+  auto corr = [&](uint32_t en) -> float {   // (exact - marker) * x[col]
+    const uint32_t col = min(en & 0xFFFFu, (uint32_t)in_f - 1);
+    const uint32_t bits = en >> 16;
+    return (bf16lo_to_f32(bits) - bf16lo_to_f32(bits & 0x807Fu)) * x_at(col);
+  };
+
+  // prologue: offsets of rows 0 and 1, paired x (registers), the first two
+  // passes, the entries of row 0; x to LDS
+  uint32_t ob0 = 0, ob1 = 0, on0 = 0, on1 = 0;
+  if constexpr (OVF) {
+    load_off(0, ob0, ob1);
+    load_off(1, on0, on1);
+  }
+  const __amdgpu_buffer_rsrc_t rx = rsrc(xp, (uint64_t)in_f * 2);
+  u32x4 xs[XS][4];
+#pragma unroll
+  for (int i = 0; i < XS; ++i) {
+    const uint32_t a = (uint32_t)min((int64_t)(threadIdx.x + 256 * i), P - 1);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) xs[i][q] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(a * 64 + 16 * q), 0, 0);
+  }
+  GgufRaw R[2];
+  load_pass(0, 0, R[0]);
+  load_pass(0, 1, R[1]);
+  uint32_t ent[NB] = {};
+  if constexpr (OVF) load_ents(ob0, ob1, ent);
+#pragma unroll
+  for (int i = 0; i < XS; ++i) {
+    const int a = threadIdx.x + 256 * i;
+    if (a < NP * 64) {
+      u32x4* dst = (u32x4*)lds + (a >> 6) * 4 * 64 + (a & 63);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[q * 64] = xs[i][q];
+    }
+  }
+  __syncthreads();
+
+  const u32x4* xl = (const u32x4*)lds + lane;
+  float acc0 = 0.f, acc1 = 0.f;
+  bool more = false;
+  int nparked = 0;
+  auto do_row = [&](int i, auto par) {
+    constexpr int PAR = decltype(par)::value;
+#pragma unroll
+    for (int c = 0; c < NP; ++c) {
+      GgufRaw& cur = R[(PAR + c) & 1];
+      uint32_t w[16];
+      decode_pairs<true>(gguf_atom(cur), w);
+      float t0 = 0.f, t1 = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 v = xl[(c * 4 + q) * 64];
+        t0 = dot2_bf16(w[4 * q + 0], v.x, t0);
+        t1 = dot2_bf16(w[4 * q + 1], v.y, t1);
+        t0 = dot2_bf16(w[4 * q + 2], v.z, t0);
+        t1 = dot2_bf16(w[4 * q + 3], v.w, t1);
+      }
+      if (c < NP - 1 || (int64_t)(64 * c + lane) < P) {
+        acc0 += t0;
+        acc1 += t1;
+      }
+      if (c + 2 < NP) load_pass(i, c + 2, cur);
+      else load_pass(i + 1, c + 2 - NP, cur);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (OVF) {
+#pragma unroll
+      for (int k = 0; k < NB; ++k) {
+        const float cc = corr(ent[k]);
+        acc0 += (ob0 + (uint32_t)(lane + 64 * k) < ob1) ? cc : 0.f;
+      }
+      more = __builtin_amdgcn_readfirstlane(ob1) > __builtin_amdgcn_readfirstlane(ob0) + 64u * NB;
+      uint32_t nn0, nn1;
+      load_off(i + 2, nn0, nn1);
+      load_ents(on0, on1, ent);
+      ob0 = on0; ob1 = on1; on0 = nn0; on1 = nn1;
+    }
+    const float tot = wave_sum_dpp(acc0 + acc1);
+    const int64_t r = base + 4 * (int64_t)i;
+    if (OVF && more) {
+      if (lane == 63) {
+        dpart[wave][nparked] = tot;
+        drow[wave][nparked] = i;
+      }
+      ++nparked;
+    } else if (lane == 63 && r < out_f) {
+      if constexpr (YF32) ((float*)y)[r] = tot;
+      else ((uint16_t*)y)[r] = (uint16_t)f32_to_bf16_rne(tot);
+    }
+    acc0 = 0.f;
+    acc1 = 0.f;
+  };
+  if constexpr (NP % 2 == 0) {
+    for (int i = 0; i < iters; ++i) do_row(i, std::integral_constant<int, 0>{});
+  } else {
+    int i = 0;
+    for (; i + 1 < iters; i += 2) {
+      do_row(i, std::integral_constant<int, 0>{});
+      do_row(i + 1, std::integral_constant<int, 1>{});
+    }
+    if (i < iters) do_row(i, std::integral_constant<int, 0>{});
+  }
+  for (int d = 0; d < nparked; ++d) {            // rows with more entries than the read-ahead
+    const int i = __builtin_amdgcn_readfirstlane(drow[wave][d]);
+    const int64_t r = base + 4 * (int64_t)i;
+    const uint32_t b0 = ovf_off[row_of(i)], b1 = ovf_off[row_of(i) + 1];
+    float a = 0.f;
+    for (uint32_t e = b0 + 64u * NB + (uint32_t)lane; e < b1; e += 64) a += corr(ovf_ent[e]);
+    const float tot = wave_sum_dpp(a) + dpart[wave][d];
+    if (lane == 63 && r < out_f) {
+      if constexpr (YF32) ((float*)y)[r] = tot;
+      else ((uint16_t*)y)[r] = (uint16_t)f32_to_bf16_rne(tot);
+    }
+  }
+}
+
 }  // namespace gguf
 }  // namespace bf16x
 
@@ -275,6 +454,12 @@ int gguf_decode_launch(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, in
   return launch_status();
 }
 
+// BF16X_GGUF_LONG=0 keeps every shape on the one-pass-ahead kernel.
+bool long_enabled() {
+  static const bool v = getenv("BF16X_GGUF_LONG") == nullptr || atoi(getenv("BF16X_GGUF_LONG")) != 0;
+  return v;
+}
+
 int gguf_gemv_launch(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes, int64_t out_f,
                      int64_t in_f, const uint32_t* ovf_off, const uint32_t* ovf_ent, void* y, int32_t y_dtype,
                      void* workspace, int64_t workspace_bytes, hipStream_t st) {
@@ -289,6 +474,36 @@ int gguf_gemv_launch(const void* x, int32_t x_dtype, const uint8_t* blocks, int6
   uint32_t* xp = (uint32_t*)workspace;
   hipLaunchKernelGGL(x_pairs_kernel, dim3((unsigned)((in_f / 2 + 255) / 256)), dim3(256), 0, st, (const uint16_t*)x,
                      in_f, xp);
+  const int64_t P = in_f / 32;
+  const int np = (int)((P + 63) / 64);
+  if (long_enabled() && P % 2 == 0 && np >= 3 && np <= 16) {
+    // rows per wave (as the dict GEMV): 4 from 2048 groups of 4 rows, 2 from 1024
+    const int64_t groups = (out_f + 3) / 4;
+    int iters = groups >= 2048 ? 4 : (groups >= 1024 ? 2 : 1);
+    if (const char* e = getenv("BF16X_GGUF_ITERS")) iters = std::max(1, std::min(atoi(e), kLongMaxIters));
+    const int64_t lgrid = (groups + iters - 1) / iters;
+    const size_t lds = (size_t)np * 4 * 64 * 16;
+    const int xs = (np * 64 + 255) / 256;
+#define BF16X_GL1(NP_, XS_, YF_, OV_)                                                                           \
+  hipLaunchKernelGGL((gguf_gemv_long_kernel<NP_, XS_, YF_, OV_>), dim3((unsigned)lgrid), dim3(256), lds, st, blocks, \
+                     xp, out_f, in_f, ovf_off, ovf_ent, iters, y)
+#define BF16X_GL(NP_)                                                                                           \
+  case NP_:                                                                                                     \
+    if (ovf_off) { if (y_dtype == BF16X_F32) BF16X_GL1(NP_, (NP_ * 64 + 255) / 256, true, true);               \
+                   else BF16X_GL1(NP_, (NP_ * 64 + 255) / 256, false, true); }                                  \
+    else { if (y_dtype == BF16X_F32) BF16X_GL1(NP_, (NP_ * 64 + 255) / 256, true, false);                      \
+           else BF16X_GL1(NP_, (NP_ * 64 + 255) / 256, false, false); }                                         \
+    break;
+    (void)xs;
+    switch (np) {
+      BF16X_GL(3) BF16X_GL(4) BF16X_GL(5) BF16X_GL(6) BF16X_GL(7) BF16X_GL(8) BF16X_GL(9) BF16X_GL(10)
+      BF16X_GL(11) BF16X_GL(12) BF16X_GL(13) BF16X_GL(14) BF16X_GL(15) BF16X_GL(16)
+      default: break;
+    }
+#undef BF16X_GL
+#undef BF16X_GL1
+    return launch_status();
+  }
   const dim3 g((unsigned)grid), b(256);
   if (ovf_off) {
     if (y_dtype == BF16X_F32)
