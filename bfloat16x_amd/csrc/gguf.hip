@@ -232,9 +232,11 @@ __global__ __launch_bounds__(256) void gguf_gemv_kernel(const uint8_t* __restric
 // GEMV for rows of 64k columns (k >= 3, in_f <= 32768): the dict GEMV's
 // long-row structure (gemv.hip, gemv_long_kernel).  One wave per row, the
 // row streamed in NP passes of 64 blocks through a two-slot register ring
-// that runs on across the wave's rows; paired x staged once per workgroup in
-// LDS (lane-major: chunk (4 pass + q) * 64 + lane holds pair words 4q .. 4q+3
-// of block 64 pass + lane); workgroup rows base + 4 i + wave, i < iters.  The
+// that runs on across the wave's rows; x (bf16, 4-byte aligned) is read once
+// per workgroup, rearranged into the decoder's pair order in registers and
+// staged in LDS (lane-major: chunk (4 pass + q) * 64 + lane holds pair words
+// 4q .. 4q+3 of block 64 pass + lane), so no separate x launch is needed;
+// workgroup rows base + 4 i + wave, i < iters.  The
 // row's base byte offset is a multiple of 4 (P even), so it enters the loads
 // as a scalar offset and the 2-byte skew of a block is its lane's.  OVF: the
 // side-table entries of a row (first 64 NP read one row ahead, the rest after
@@ -243,7 +245,7 @@ constexpr int kLongMaxIters = 16;
 
 template <int NP, int XS, bool YF32, bool OVF>
 __global__ __launch_bounds__(256) void gguf_gemv_long_kernel(const uint8_t* __restrict__ blocks,
-                                                             const uint32_t* __restrict__ xp, int64_t out_f,
+                                                             const uint16_t* __restrict__ x, int64_t out_f,
                                                              int64_t in_f, const uint32_t* __restrict__ ovf_off,
                                                              const uint32_t* __restrict__ ovf_ent, int iters,
                                                              void* __restrict__ y) {
@@ -300,8 +302,8 @@ __global__ __launch_bounds__(256) void gguf_gemv_long_kernel(const uint8_t* __re
     load_off(0, ob0, ob1);
     load_off(1, on0, on1);
   }
-  const __amdgpu_buffer_rsrc_t rx = rsrc(xp, (uint64_t)in_f * 2);
-  u32x4 xs[XS][4];
+  const __amdgpu_buffer_rsrc_t rx = rsrc(x, (uint64_t)in_f * 2);
+  u32x4 xs[XS][4];                              // block a's 32 x values, natural order
 #pragma unroll
   for (int i = 0; i < XS; ++i) {
     const uint32_t a = (uint32_t)min((int64_t)(threadIdx.x + 256 * i), P - 1);
@@ -317,9 +319,20 @@ __global__ __launch_bounds__(256) void gguf_gemv_long_kernel(const uint8_t* __re
   for (int i = 0; i < XS; ++i) {
     const int a = threadIdx.x + 256 * i;
     if (a < NP * 64) {
+      // natural -> pair order: word j = x[32a + j] | x[32a + 16 + j] << 16
+      const uint32_t lo[8] = {xs[i][0].x, xs[i][0].y, xs[i][0].z, xs[i][0].w,
+                              xs[i][1].x, xs[i][1].y, xs[i][1].z, xs[i][1].w};
+      const uint32_t hi[8] = {xs[i][2].x, xs[i][2].y, xs[i][2].z, xs[i][2].w,
+                              xs[i][3].x, xs[i][3].y, xs[i][3].z, xs[i][3].w};
+      uint32_t pw[16];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        pw[2 * k] = perm(hi[k], lo[k], 0x05040100u);
+        pw[2 * k + 1] = perm(hi[k], lo[k], 0x07060302u);
+      }
       u32x4* dst = (u32x4*)lds + (a >> 6) * 4 * 64 + (a & 63);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) dst[q * 64] = xs[i][q];
+      for (int q = 0; q < 4; ++q) dst[q * 64] = u32x4{pw[4 * q], pw[4 * q + 1], pw[4 * q + 2], pw[4 * q + 3]};
     }
   }
   __syncthreads();
@@ -472,11 +485,9 @@ int gguf_gemv_launch(const void* x, int32_t x_dtype, const uint8_t* blocks, int6
   const int64_t grid = (out_f + 3) / 4;
   if (grid > INT32_MAX) return BF16X_ESHAPE;
   uint32_t* xp = (uint32_t*)workspace;
-  hipLaunchKernelGGL(x_pairs_kernel, dim3((unsigned)((in_f / 2 + 255) / 256)), dim3(256), 0, st, (const uint16_t*)x,
-                     in_f, xp);
   const int64_t P = in_f / 32;
   const int np = (int)((P + 63) / 64);
-  if (long_enabled() && P % 2 == 0 && np >= 3 && np <= 16) {
+  if (long_enabled() && P % 2 == 0 && np >= 3 && np <= 16 && aligned4(x)) {
     // rows per wave (as the dict GEMV): 4 from 2048 groups of 4 rows, 2 from 1024
     const int64_t groups = (out_f + 3) / 4;
     int iters = groups >= 2048 ? 4 : (groups >= 1024 ? 2 : 1);
@@ -486,7 +497,7 @@ int gguf_gemv_launch(const void* x, int32_t x_dtype, const uint8_t* blocks, int6
     const int xs = (np * 64 + 255) / 256;
 #define BF16X_GL1(NP_, XS_, YF_, OV_)                                                                           \
   hipLaunchKernelGGL((gguf_gemv_long_kernel<NP_, XS_, YF_, OV_>), dim3((unsigned)lgrid), dim3(256), lds, st, blocks, \
-                     xp, out_f, in_f, ovf_off, ovf_ent, iters, y)
+                     (const uint16_t*)x, out_f, in_f, ovf_off, ovf_ent, iters, y)
 #define BF16X_GL(NP_)                                                                                           \
   case NP_:                                                                                                     \
     if (ovf_off) { if (y_dtype == BF16X_F32) BF16X_GL1(NP_, (NP_ * 64 + 255) / 256, true, true);               \
@@ -504,6 +515,8 @@ int gguf_gemv_launch(const void* x, int32_t x_dtype, const uint8_t* blocks, int6
 #undef BF16X_GL1
     return launch_status();
   }
+  hipLaunchKernelGGL(x_pairs_kernel, dim3((unsigned)((in_f / 2 + 255) / 256)), dim3(256), 0, st, (const uint16_t*)x,
+                     in_f, xp);
   const dim3 g((unsigned)grid), b(256);
   if (ovf_off) {
     if (y_dtype == BF16X_F32)
