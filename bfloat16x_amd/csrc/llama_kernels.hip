@@ -267,21 +267,33 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t* __rest
   __shared__ int last;
   const int g = blockIdx.x, sp = blockIdx.y, S = gridDim.y;
   const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
-  const int p = pos[0];
-  const bool cur = p >= 0 && p < max_len;                        // the new row fits in the cache
-  const int n_old = p < 0 ? 0 : (p > max_len ? max_len : p);     // cached keys 0 .. n_old - 1
-  const int n = n_old + (cur ? 1 : 0);
-  const int chunk = (n + S - 1) / S;
-  const int j0 = sp * chunk < n ? sp * chunk : n;
-  const int j1 = j0 + chunk < n ? j0 + chunk : n;
-  const int jc = j1 < n_old ? j1 : n_old;                        // end of the cached keys of the range
-  // The K and V rows of the first 64 keys of the range are loaded before
-  // anything else so that their latency overlaps the rotary step.
+  // Key ranges are fixed by the cache length, not by the position: range sp
+  // is [sp * chunk, (sp + 1) * chunk) cut to the n keys in use, so the K and V
+  // rows of its first 64 keys are requested at entry, together with the
+  // position, and their latency overlaps the position's and the rotary step.
+  const int chunk = (max_len + S - 1) / S;
+  const int jf = sp * chunk;
   const int q4 = tid & 3;
   const uint16_t* K = kc + (int64_t)g * max_len * 128;
   const uint32_t* V = (const uint32_t*)(vc + (int64_t)g * max_len * 128);
   u32x4 kraw[4];
   uint32_t vraw[16];
+  {
+    // rows past the keys in use are read (clamped into the cache) and never used
+    const int jk = min(jf + (tid >> 2), max_len - 1);
+    const u32x4* kr = (const u32x4*)(K + (int64_t)jk * 128 + 32 * q4);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) kraw[c] = kr[c];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) vraw[u] = V[(int64_t)min(jf + wv + 4 * u, max_len - 1) * 64 + lane];
+  }
+  const int p = pos[0];
+  const bool cur = p >= 0 && p < max_len;                        // the new row fits in the cache
+  const int n_old = p < 0 ? 0 : (p > max_len ? max_len : p);     // cached keys 0 .. n_old - 1
+  const int n = n_old + (cur ? 1 : 0);
+  const int j0 = jf < n ? jf : n;
+  const int j1 = j0 + chunk < n ? j0 + chunk : n;
+  const int jc = j1 < n_old ? j1 : n_old;                        // end of the cached keys of the range
   auto load_k = [&](int base) {
     const int j = base + (tid >> 2);
     const u32x4* kr = (const u32x4*)(K + (int64_t)(j < jc ? j : 0) * 128 + 32 * q4);
@@ -295,8 +307,6 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(const uint16_t* __rest
       vraw[u] = j < jc ? V[(int64_t)j * 64 + lane] : 0u;
     }
   };
-  load_k(j0);
-  load_v(j0 + wv);
   // 0. rotary embedding, KV append
   {
     const int pc = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
