@@ -71,6 +71,11 @@ PROTOTYPES = {
                                        _c_i64, _P, _P, _P, _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
     "bf16x_gemv_swiglu": (ctypes.c_int, [_P, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P, _P, _c_i64,
                                          _c_i64, _c_i32, _P, _P]),
+    "bf16x_gemv_residual_slots": (_c_i64, [_c_i64, _c_i64]),
+    "bf16x_gemv_residual": (ctypes.c_int, [_P, _P, _P, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
+                                           _P, _P, _P, _c_i64, _c_i64, _c_i32, _P, _P]),
+    "bf16x_gemv_prenormed": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
+                                            _P, _c_i64, _P, _P, _P, _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
     "bf16x_greedy": (ctypes.c_int, [_P, _c_i64, _P, _P, _P, _c_i64, _P]),
 }
 

@@ -139,20 +139,54 @@ __device__ __forceinline__ Atom load_atom_buf(__amdgpu_buffer_rsrc_t rs, __amdgp
 // the roundings of the standalone RMSNorm kernel (bf16(bf16(h * rsqrt(mean
 // (h^2) + eps)) * w)); workgroup 0 also stores h to res_out (a buffer no
 // workgroup of this launch reads).
+// XM = 2 (pre-summed RMSNorm staging): x is h itself and the sum of h^2 comes
+// from the slots a RES = 1 launch left (NormArgs::slots / nslots): the
+// staging only scales.
 struct NormArgs {
   const uint16_t* res_in;
   const uint16_t* w;
   uint16_t* res_out;
   float eps;
+  const float* slots;   // XM = 2: partial sums of squares of x, summed in slot order
+  int nslots;
 };
 
-template <int NS, int G, int XT, bool EXACT, bool FULL, int EPI = 0, int XM = 0>
+// RES = 1 (G = 1): the residual epilogue.  Row r's output y_r (stored as
+// bf16) is added to the residual stream, h_r = bf16(y_r + res_in[r]) goes to
+// res_out[r], and workgroup b stores the sum of h_r^2 over its rows to
+// slots[b] (its waves' sums added in wave order): the next projection's
+// RMSNorm (XM = 2) then needs no pass of its own over h.
+struct ResArgs {
+  const uint16_t* res_in;
+  uint16_t* res_out;
+  float* slots;
+};
+
+// Sum of slots[0 .. n), n <= 64 kMaxSlotsPerLane, in a fixed order: lane l
+// adds slots l, l + 64, ... (all loaded first, so their latencies overlap),
+// then the DPP wave sum; the same in every wave, returned in all lanes.
+constexpr int kMaxSlotsPerLane = 16;
+struct SlotLoads { float v[kMaxSlotsPerLane]; };
+__device__ __forceinline__ void slot_load(const float* __restrict__ slots, int n, int lane, SlotLoads& sl) {
+#pragma unroll
+  for (int k = 0; k < kMaxSlotsPerLane; ++k) sl.v[k] = slots[min(lane + 64 * k, n - 1)];
+}
+__device__ __forceinline__ float slot_sum(const SlotLoads& sl, int n, int lane) {
+  float v = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxSlotsPerLane; ++k) v += (lane + 64 * k < n) ? sl.v[k] : 0.f;
+  v = wave_sum_dpp(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+template <int NS, int G, int XT, bool EXACT, bool FULL, int EPI = 0, int XM = 0, int RES = 0>
 __global__ __launch_bounds__(256) void gemv_pipe_kernel(
     const void* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
     const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
     const uint32_t* __restrict__ tile_off, const uint32_t* __restrict__ tile_ent,
     const uint8_t* __restrict__ tile_sat, int64_t out_f, int64_t in_f, int iters, uint16_t* __restrict__ y,
-    NormArgs na = NormArgs{nullptr, nullptr, nullptr, 0.f}) {
+    NormArgs na = NormArgs{nullptr, nullptr, nullptr, 0.f, nullptr, 0}, ResArgs ra = ResArgs{nullptr, nullptr, nullptr}) {
+  static_assert(RES == 0 || (G == 1 && EPI == 0), "the residual epilogue is for one wave per row");
   constexpr int RPI = 4 / G;                              // rows per workgroup iteration
   constexpr int XW = (XT == BF16X_BF16) ? 16 : 32;        // x words per atom
   constexpr int NC = XW / 4;                              // 16-byte chunks per atom
@@ -243,13 +277,20 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
     load_off(rn, ebn, een);
   }
   constexpr int XSLOTS = (G * APW + 255) / 256;  // x atoms staged per thread (<= 2)
+  [[maybe_unused]] SlotLoads slot_v;
+  if constexpr (XM == 2) slot_load(na.slots, na.nslots, lane, slot_v);   // first: the norm waits for them
   uint32_t xs_reg[XSLOTS][XW];
-  [[maybe_unused]] uint32_t wn_reg[XM == 1 ? XSLOTS : 1][XM == 1 ? XW : 1];
+  [[maybe_unused]] uint32_t wn_reg[XM != 0 ? XSLOTS : 1][XM != 0 ? XW : 1];
   [[maybe_unused]] float ssq = 0.f;
 #pragma unroll
   for (int i = 0; i < XSLOTS; ++i) {
     const int slot = threadIdx.x + 256 * i;
-    if constexpr (XM == 1) {
+    if constexpr (XM == 2) {
+      static_assert(XT == BF16X_BF16, "the RMSNorm staging takes bf16 x");
+      const int64_t a = min((int64_t)slot, P - 1);
+      load_x_atom<XT>(x, a, xs_reg[i]);                    // h, pair order
+      load_x_atom<XT>(na.w, a, wn_reg[i]);
+    } else if constexpr (XM == 1) {
       static_assert(XT == BF16X_BF16, "the RMSNorm staging takes bf16 x");
       const int64_t a = min((int64_t)slot, P - 1);
       const uint16_t* xa = (const uint16_t*)x + 32 * a;
@@ -296,14 +337,19 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
   load_row(r, bufA);
   // the first row's entries go out before the staging waits (XM = 1 waits for
   // its loads and a barrier before the x stores)
-  if constexpr (EXACT && XM == 1) load_ents(eb, ee, entA, satA);
-  if constexpr (XM == 1) {
+  if constexpr (EXACT && XM != 0) load_ents(eb, ee, entA, satA);
+  if constexpr (XM != 0) {
     // sum of squares over the row, then x = bf16(bf16(h * s) * w) in place
-    __shared__ float nred[4];
-    float v = wave_sum_dpp(ssq);
-    if (lane == 63) nred[wave] = v;
-    __syncthreads();
-    const float tot = (nred[0] + nred[1]) + (nred[2] + nred[3]);
+    float tot;
+    if constexpr (XM == 2) {
+      tot = slot_sum(slot_v, na.nslots, lane);
+    } else {
+      __shared__ float nred[4];
+      float v = wave_sum_dpp(ssq);
+      if (lane == 63) nred[wave] = v;
+      __syncthreads();
+      tot = (nred[0] + nred[1]) + (nred[2] + nred[3]);
+    }
     const float sc = 1.0f / sqrtf(tot / (float)in_f + na.eps);
 #pragma unroll
     for (int i = 0; i < XSLOTS; ++i)
@@ -330,9 +376,14 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
 
   const u32x4* xl = (const u32x4*)lds + (int64_t)(g * NS) * NC * 64 + lane;
   float gate_keep = 0.f;                                  // EPI = 1: this wave's gate output
+  [[maybe_unused]] float res_ss = 0.f;                    // RES = 1: sum of h^2 of this wave's rows (lane 63)
   auto body = [&](auto prefetch, int it, Atom* cur, uint32_t* ent, uint8_t* sat, Atom* nxt, uint32_t* entn,
                   uint8_t* satn) {
     constexpr bool PF = decltype(prefetch)::value;
+    // RES: this row's residual, requested before the prefetch so that waiting
+    // for it at the store does not wait for the next row's loads
+    [[maybe_unused]] uint32_t rin = 0;
+    if constexpr (RES == 1) rin = ra.res_in[min(r, out_f - 1)];
     // prefetch: offsets two rows ahead, then the next row's entries and atoms
     const int64_t rnn = rn + RPI;
     uint32_t ebnn = 0, eenn = 0;
@@ -394,7 +445,15 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
         y[(r >> 3) * 4 + (r & 3)] = (uint16_t)f32_to_bf16_rne(sg * yb);
       }
     } else if constexpr (G == 1) {
-      if (lane == 63 && r < out_f) y[r] = (uint16_t)f32_to_bf16_rne(tot);
+      if (lane == 63 && r < out_f) {
+        const uint32_t yb = f32_to_bf16_rne(tot);
+        y[r] = (uint16_t)yb;
+        if constexpr (RES == 1) {
+          const float h = bf16lo_to_f32(f32_to_bf16_rne(bf16lo_to_f32(yb) + bf16lo_to_f32(rin)));
+          ra.res_out[r] = (uint16_t)(__float_as_uint(h) >> 16);
+          res_ss += h * h;
+        }
+      }
     } else {
       if (lane == 63) part[it & 1][wave] = tot;
       __syncthreads();
@@ -419,6 +478,12 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
   } else {
     body(std::false_type{}, it, bufA, entA, satA, bufB, entB, satB);
   }
+  if constexpr (RES == 1) {
+    __shared__ float rpart[4];
+    if (lane == 63) rpart[wave] = res_ss;
+    __syncthreads();
+    if (threadIdx.x == 0) ra.slots[blockIdx.x] = (rpart[0] + rpart[1]) + (rpart[2] + rpart[3]);
+  }
 }
 
 // Long rows (in_f > 4096, bf16 x): one wave per row, the row streamed in NP
@@ -435,12 +500,13 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
 // would make the compiler keep the whole pass schedule's registers live).
 constexpr int kLongMaxIters = 16;
 
-template <int NP, int XS, bool EXACT, bool FULL>
+template <int NP, int XS, bool EXACT, bool FULL, int RES = 0>
 __global__ __launch_bounds__(256) void gemv_long_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
     const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
     const uint32_t* __restrict__ tile_off, const uint32_t* __restrict__ tile_ent,
-    const uint8_t* __restrict__ tile_sat, int64_t out_f, int64_t in_f, int iters, uint16_t* __restrict__ y) {
+    const uint8_t* __restrict__ tile_sat, int64_t out_f, int64_t in_f, int iters, uint16_t* __restrict__ y,
+    ResArgs ra = ResArgs{nullptr, nullptr, nullptr}) {
   static_assert(NP >= 2, "at least two passes per row");
   constexpr int NB = NP;                        // entry batches of 64 read ahead per row (3.1 % of it)
   extern __shared__ uint32_t lds[];
@@ -520,10 +586,24 @@ __global__ __launch_bounds__(256) void gemv_long_kernel(
   float acc0 = 0.f, acc1 = 0.f;
   bool more = false;                            // uniform: the row has entries past the batches
   int nparked = 0;                              // uniform
+  [[maybe_unused]] float res_ss = 0.f;          // RES = 1: sum of h^2 of this wave's rows (lane 63)
+  auto store_row = [&](int64_t r, float tot, uint32_t rin) {  // lane 63; rin: the row's residual
+    const uint32_t yb = f32_to_bf16_rne(tot);
+    y[r] = (uint16_t)yb;
+    if constexpr (RES == 1) {
+      const float h = bf16lo_to_f32(f32_to_bf16_rne(bf16lo_to_f32(yb) + bf16lo_to_f32(rin)));
+      ra.res_out[r] = (uint16_t)(__float_as_uint(h) >> 16);
+      res_ss += h * h;
+    }
+  };
   // row i; its pass c sits in ring slot (PAR + c) % 2 and is refilled with
   // the pass two ahead (in this row or the next) once decoded
   auto do_row = [&](int i, auto par) {
     constexpr int PAR = decltype(par)::value;
+    // RES: the row's residual, requested before this row's refills so that
+    // waiting for it at the store does not wait for them
+    [[maybe_unused]] uint32_t rin = 0;
+    if constexpr (RES == 1) rin = ra.res_in[row_of(i)];
 #pragma unroll
     for (int c = 0; c < NP; ++c) {
       Atom& cur = R[(PAR + c) & 1];
@@ -572,7 +652,7 @@ __global__ __launch_bounds__(256) void gemv_long_kernel(
       }
       ++nparked;
     } else if (lane == 63 && r < out_f) {
-      y[r] = (uint16_t)f32_to_bf16_rne(tot);
+      store_row(r, tot, rin);
     }
     acc0 = 0.f;
     acc1 = 0.f;
@@ -601,7 +681,13 @@ __global__ __launch_bounds__(256) void gemv_long_kernel(
       a = fmaf(bf16lo_to_f32(en) - bf16lo_to_f32(sbits), x_at(kk), a);
     }
     const float tot = wave_sum_dpp(a) + dpart[wave][d];
-    if (lane == 63 && r < out_f) y[r] = (uint16_t)f32_to_bf16_rne(tot);
+    if (lane == 63 && r < out_f) store_row(r, tot, RES == 1 ? (uint32_t)ra.res_in[r] : 0u);
+  }
+  if constexpr (RES == 1) {
+    __shared__ float rpart[4];
+    if (lane == 63) rpart[wave] = res_ss;
+    __syncthreads();
+    if (threadIdx.x == 0) ra.slots[blockIdx.x] = (rpart[0] + rpart[1]) + (rpart[2] + rpart[3]);
   }
 }
 
@@ -669,23 +755,30 @@ bool gemv_long_enabled() {
 // Long rows (bf16 x, 4096 < in_f <= 16384): the one-wave-per-row kernel
 // (4096 x 14336 exact: 20.5 us against 22.4 us for the split-K kernel;
 // 2048 x 14336: 11.5 against 13.3).
+// rows per wave of the long-row kernel (measured): 4 from 2048 groups of 4
+// rows, 2 from 1024
+int long_iters(int64_t groups) {
+  int iters = gemv_iters_override();
+  if (iters <= 0) iters = groups >= 2048 ? 4 : (groups >= 1024 ? 2 : 1);
+  return std::min(iters, kLongMaxIters);
+}
+
+template <int RES = 0>
 int launch_gemv_long(const void* x, const uint32_t* sign, const uint32_t* mant, const uint32_t* delta,
                      const uint16_t* emax2, const uint32_t* to, const uint32_t* te, const uint8_t* ts,
-                     int64_t out_f, int64_t in_f, uint16_t* y, hipStream_t st) {
+                     int64_t out_f, int64_t in_f, uint16_t* y, hipStream_t st,
+                     ResArgs ra = ResArgs{nullptr, nullptr, nullptr}) {
   const int64_t P = in_f >> 5;
   const int np = (int)((P + 63) / 64);
   const bool full = P % 64 == 0;
   const size_t lds = (size_t)np * 4 * 64 * 16;
   const int64_t groups = (out_f + 3) / 4;
-  // rows per wave (measured): 4 from 2048 groups of 4 rows, 2 from 1024
-  int iters = gemv_iters_override();
-  if (iters <= 0) iters = groups >= 2048 ? 4 : (groups >= 1024 ? 2 : 1);
-  iters = std::min(iters, kLongMaxIters);
+  const int iters = long_iters(groups);
   const int64_t grid = (groups + iters - 1) / iters;
   if (grid > INT32_MAX) return BF16X_ESHAPE;
 #define BF16X_LONG1(NP_, EX_, FU_)                                                                              \
-  hipLaunchKernelGGL((gemv_long_kernel<NP_, 2, EX_, FU_>), dim3((unsigned)grid), dim3(256), lds, st,             \
-                     (const uint16_t*)x, sign, mant, delta, emax2, to, te, ts, out_f, in_f, iters, y)
+  hipLaunchKernelGGL((gemv_long_kernel<NP_, 2, EX_, FU_, RES>), dim3((unsigned)grid), dim3(256), lds, st,        \
+                     (const uint16_t*)x, sign, mant, delta, emax2, to, te, ts, out_f, in_f, iters, y, ra)
 #define BF16X_LONG(NP_)                                                                                        \
   case NP_:                                                                                                    \
     if (to) { if (full) BF16X_LONG1(NP_, true, true); else BF16X_LONG1(NP_, true, false); }                    \
@@ -778,10 +871,11 @@ int launch_gemv_g1(const void* x, const uint32_t* sign, const uint32_t* mant, co
   const bool full = P == (int64_t)64 * NS;
   const size_t lds = (size_t)NS * 64 * 4 * 16;
   const int64_t groups = (out_f + 3) / 4;
-  int iters = EPI == 1 ? 2 : (groups >= 2048 ? 2 : 1);
-  if (XM == 1) {
-    // every workgroup normalises x in its prologue: enough rows per
-    // workgroup that the grid fits one round of resident workgroups (4 per CU)
+  int iters = EPI == 1 ? 2 : (groups >= 1024 ? 2 : 1);
+  if (XM != 0) {
+    // every workgroup normalises x in its prologue (with its own pass over
+    // x): enough rows per workgroup that the grid fits one round of resident
+    // workgroups (4 per CU)
     const int64_t slots = 1024;
     iters = std::max<int64_t>(iters, (groups + slots - 1) / slots);
     if (EPI == 1) iters += iters & 1;
@@ -833,6 +927,101 @@ extern "C" int bf16x_gemv_swiglu(const void* x, const int32_t* sign, int64_t n_s
                               (const uint16_t*)emax, ex ? tile_off : nullptr, ex ? tile_ent : nullptr,
                               ex ? tile_sat : nullptr, out_f, in_f, y, NormArgs{nullptr, nullptr, nullptr, 0.f},
                               (hipStream_t)stream);
+}
+
+namespace {
+
+// Rows per workgroup of the one-wave-per-row pipelined kernel with the
+// residual epilogue (as launch_gemv: 2 from 1024 groups of 4 rows).
+int res_pipe_iters(int64_t groups) {
+  const int it = gemv_iters_override();
+  return it > 0 ? it : (groups >= 1024 ? 2 : 1);
+}
+
+}  // namespace
+
+// Workgroups of bf16x_gemv_residual = the slots it writes; -1 for shapes it
+// does not take.
+extern "C" int64_t bf16x_gemv_residual_slots(int64_t out_f, int64_t in_f) {
+  if (out_f <= 0 || in_f <= 0 || in_f % 32 != 0 || in_f > 16384) return -1;
+  const int64_t P = in_f >> 5, groups = (out_f + 3) / 4;
+  if ((out_f + 1) * P * 28 >= (int64_t)0xFFFFFFFF) return -1;
+  const int64_t it = P <= 128 ? res_pipe_iters(groups) : long_iters(groups);
+  return (groups + it - 1) / it;
+}
+
+extern "C" int bf16x_gemv_residual(const void* x, const uint16_t* residual_in, uint16_t* residual_out, float* slots,
+                                   int64_t n_slots, const int32_t* sign, int64_t n_sign, const int32_t* mant,
+                                   int64_t n_mant, const int32_t* delta, int64_t n_delta, const uint8_t* emax,
+                                   int64_t n_emax, const uint32_t* tile_off, const uint32_t* tile_ent,
+                                   const uint8_t* tile_sat, int64_t out_f, int64_t in_f, int32_t mode, uint16_t* y,
+                                   bf16x_stream_t stream) {
+  const int rc = check_gemv_args(x, sign, n_sign, mant, n_mant, delta, n_delta, emax, n_emax, tile_off, tile_ent,
+                                 tile_sat, out_f, in_f, mode, y);
+  if (rc) return rc;
+  if (!residual_in || !residual_out || !slots) return BF16X_EARG;
+  if ((const void*)residual_out == x || residual_out == y || (const void*)residual_in == (const void*)y)
+    return BF16X_EARG;
+  if (!aligned2(residual_in) || !aligned2(residual_out) || !aligned4(slots)) return BF16X_EARG;
+  const int64_t need = bf16x_gemv_residual_slots(out_f, in_f);
+  if (need < 0) return BF16X_ESHAPE;
+  if (n_slots < need) return BF16X_ECAPACITY;
+  const bool ex = mode == BF16X_EXACT;
+  const uint32_t *to = ex ? tile_off : nullptr, *te = ex ? tile_ent : nullptr;
+  const uint8_t* ts = ex ? tile_sat : nullptr;
+  const uint32_t* s = (const uint32_t*)sign;
+  const uint32_t* m = (const uint32_t*)mant;
+  const uint32_t* d = (const uint32_t*)delta;
+  const uint16_t* e = (const uint16_t*)emax;
+  hipStream_t st = (hipStream_t)stream;
+  const ResArgs ra{residual_in, residual_out, slots};
+  const int64_t P = in_f >> 5;
+  if (P > 128) {
+    const int r2 = launch_gemv_long<1>(x, s, m, d, e, to, te, ts, out_f, in_f, y, st, ra);
+    return r2;
+  }
+  const int NS = P > 64 ? 2 : 1;
+  const bool full = P == (int64_t)64 * NS;
+  const size_t lds = (size_t)NS * 64 * 4 * 16;
+  const int64_t groups = (out_f + 3) / 4;
+  const int iters = res_pipe_iters(groups);
+  const int64_t grid = (groups + iters - 1) / iters;
+  const NormArgs na{nullptr, nullptr, nullptr, 0.f, nullptr, 0};
+#define BF16X_R1(NS_, EX_, FULL_)                                                                                  \
+  hipLaunchKernelGGL((gemv_pipe_kernel<NS_, 1, BF16X_BF16, EX_, FULL_, 0, 0, 1>), dim3((unsigned)grid), dim3(256), lds, \
+                     st, x, s, m, d, e, to, te, ts, out_f, in_f, iters, y, na, ra)
+  if (NS == 2) {
+    if (to) { if (full) BF16X_R1(2, true, true); else BF16X_R1(2, true, false); }
+    else { if (full) BF16X_R1(2, false, true); else BF16X_R1(2, false, false); }
+  } else {
+    if (to) { if (full) BF16X_R1(1, true, true); else BF16X_R1(1, true, false); }
+    else { if (full) BF16X_R1(1, false, true); else BF16X_R1(1, false, false); }
+  }
+#undef BF16X_R1
+  return launch_status();
+}
+
+extern "C" int bf16x_gemv_prenormed(const void* h, const uint16_t* norm_weight, float eps, const float* slots,
+                                    int64_t n_slots, const int32_t* sign, int64_t n_sign, const int32_t* mant,
+                                    int64_t n_mant, const int32_t* delta, int64_t n_delta, const uint8_t* emax,
+                                    int64_t n_emax, const uint32_t* tile_off, const uint32_t* tile_ent,
+                                    const uint8_t* tile_sat, int64_t out_f, int64_t in_f, int32_t mode,
+                                    int32_t epilogue, uint16_t* y, bf16x_stream_t stream) {
+  const int rc = check_gemv_args(h, sign, n_sign, mant, n_mant, delta, n_delta, emax, n_emax, tile_off, tile_ent,
+                                 tile_sat, out_f, in_f, mode, y);
+  if (rc) return rc;
+  if (!norm_weight || !slots || n_slots <= 0 || (epilogue != 0 && epilogue != 1)) return BF16X_EARG;
+  if (n_slots > 64 * kMaxSlotsPerLane) return BF16X_ECAPACITY;
+  if (!aligned4(norm_weight) || !aligned4(slots)) return BF16X_EARG;
+  const bool ex = mode == BF16X_EXACT;
+  const NormArgs na{nullptr, norm_weight, nullptr, eps, slots, (int)n_slots};
+  const uint32_t *to = ex ? tile_off : nullptr, *te = ex ? tile_ent : nullptr;
+  const uint8_t* ts = ex ? tile_sat : nullptr;
+  if (epilogue == 1)
+    return launch_gemv_g1<1, 2>(h, (const uint32_t*)sign, (const uint32_t*)mant, (const uint32_t*)delta,
+                                (const uint16_t*)emax, to, te, ts, out_f, in_f, y, na, (hipStream_t)stream);
+  return launch_gemv_g1<0, 2>(h, (const uint32_t*)sign, (const uint32_t*)mant, (const uint32_t*)delta,
+                              (const uint16_t*)emax, to, te, ts, out_f, in_f, y, na, (hipStream_t)stream);
 }
 
 extern "C" int bf16x_gemv_norm(const void* x, const uint16_t* residual_in, const uint16_t* norm_weight,

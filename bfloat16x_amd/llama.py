@@ -19,9 +19,15 @@ device-resident state:
   * q/k/v and gate/up are single fused linears, so batch-1 decode runs 4
     GEMVs per layer; gate_up's rows are stored in groups of 8 [gate 4b ..
     4b+3, up 4b .. 4b+3] (pairs8_rows) so that the BF16X gate_up GEMV applies
-    SwiGLU in its epilogue (bf16x_gemv_swiglu): 7 launches per layer (5 with
-    norm_in_gemv, which folds each RMSNorm into the following GEMV and is
-    off by default: it measured no faster).
+    SwiGLU in its epilogue (bf16x_gemv_swiglu): 7 launches per layer;
+  * by default a BF16X decode step runs 5 launches per layer: the o and down
+    GEMVs add their output to the residual stream and leave per-workgroup
+    sums of squares (bf16x_gemv_residual), and the qkv / gate_up GEMVs
+    normalise their input from those sums (bf16x_gemv_prenormed), so no
+    RMSNorm launch remains inside the stack (residual_norm; 3.15 against
+    3.21 ms/token with the standalone RMSNorm launches).  norm_in_gemv, where
+    every GEMV workgroup also recomputes the sum of squares itself, measured
+    no faster and is off by default.
 
 Shapes of the benchmark configuration (the defaults of LlamaConfig): 32
 layers, hidden 4096, FFN 14336 (SwiGLU), 32 query / 8 KV heads, head_dim 128,
@@ -252,6 +258,15 @@ def _swiglu_gemv_ok(mod) -> bool:
     return _norm_gemv_ok(mod) and mod.out_features % 8 == 0
 
 
+def _residual_gemv_ok(mod) -> bool:
+    """A deployed BF16X o / down projection the residual-epilogue GEMV can run,
+    with few enough slots (<= 1024) for bf16x_gemv_prenormed to read."""
+    from .nn import Bf16xFused
+    n = int(_lib.lib().bf16x_gemv_residual_slots(mod.out_features, mod.in_features)) \
+        if isinstance(mod, Bf16xFused) else -1
+    return isinstance(mod, Bf16xFused) and mod.mode == "fused" and mod._bias is None and 0 < n <= 1024
+
+
 def _device(device):
     if device is None:
         if not torch.cuda.is_available():
@@ -314,7 +329,7 @@ class LlamaRunner:
     history and advances the position."""
 
     def __init__(self, model: LlamaStack, max_len: int, max_new: int, max_prompt: int | None = None,
-                 norm_in_gemv: bool = False):
+                 norm_in_gemv: bool = False, residual_norm: bool = True):
         cfg = model.cfg
         self.model, self.cfg = model, cfg
         dev = model.device
@@ -349,9 +364,21 @@ class LlamaRunner:
         # 40.2 us vs 32.5 + 5.3 us, qkv 14.7 vs 15.3 us; 3.43 vs 3.37 ms/token)
         self.fused_norm = bool(norm_in_gemv) and self.fused_decode_attention and all(
             _norm_gemv_ok(lay.qkv) and _swiglu_gemv_ok(lay.gate_up) for lay in model.layers)
+        # residual_norm (default, BF16X stacks): the o and down GEMVs add their output to the residual stream
+        # and leave per-workgroup sums of squares (bf16x_gemv_residual); the next qkv / gate_up GEMV normalises
+        # its input from them (bf16x_gemv_prenormed): no RMSNorm launch inside the stack, 5 launches per layer
+        self.res_norm = (bool(residual_norm) and not self.fused_norm and self.fused_decode_attention and all(
+            _norm_gemv_ok(lay.qkv) and _swiglu_gemv_ok(lay.gate_up) and _residual_gemv_ok(lay.o)
+            and _residual_gemv_ok(lay.down) for lay in model.layers))
         self.res_a = torch.empty(cfg.hidden, **bf)
         self.res_b = torch.empty(cfg.hidden, **bf)
         self.qkv_buf = torch.empty(cfg.qkv_rows, **bf)
+        if self.res_norm:
+            lay0 = model.layers[0]
+            self.n_slots_o = ops.gemv_residual_slots(lay0.o.out_features, lay0.o.in_features)
+            self.n_slots_down = ops.gemv_residual_slots(lay0.down.out_features, lay0.down.in_features)
+            self.slots = torch.zeros(max(self.n_slots_o, self.n_slots_down), dtype=torch.float32, device=dev)
+            self.proj_out = torch.empty(cfg.hidden, **bf)     # o / down outputs (only h is used)
         self._prompt_len = 0
 
     def _decode_fused(self, pos: torch.Tensor, ids: torch.Tensor):
@@ -383,6 +410,38 @@ class LlamaRunner:
             cur = 1 - cur
             prev = lay.down(self.act[0])
         return prev, R[cur]
+
+    def _decode_resnorm(self, pos: torch.Tensor, ids: torch.Tensor) -> torch.Tensor:
+        """One decode token with the residual adds and the RMSNorm statistics
+        carried by the projections: per layer qkv GEMV (normalising its input
+        from the previous down GEMV's sums of squares; the first layer takes
+        the embedding's RMSNorm), attention, o GEMV (+ residual, sums of
+        squares), gate_up GEMV (normalised input, SwiGLU), down GEMV (+
+        residual, sums of squares).  Returns h after the last layer."""
+        cfg, m = self.cfg, self.model
+        H, KV = cfg.n_heads, cfg.n_kv_heads
+        R = (self.res_a, self.res_b)
+        cur = 0
+        rmsnorm(m.embed, m.layers[0].attn_norm, self.normed, R[0], row_idx=ids, flags=NORM_STORE, eps=cfg.eps)
+        for i, lay in enumerate(m.layers):
+            q, o, g, d = lay.qkv, lay.o, lay.gate_up, lay.down
+            if i == 0:
+                qkv = q(self.normed[0])
+            else:
+                qkv = ops.bf16x_gemv_prenormed(R[cur], lay.attn_norm, cfg.eps, self.slots, self.n_slots_down, q._sign,
+                                               q._mant, q._delta, q._emax, q.out_features, q.in_features,
+                                               plan=q._plan, out=self.qkv_buf)
+            attention_decode(qkv, pos, self.cos_sin, H, KV, self.k_cache[i], self.v_cache[i], self.attn, self.dec_ws)
+            ops.bf16x_gemv_residual(self.attn[0], R[cur], R[1 - cur], self.slots, o._sign, o._mant, o._delta, o._emax,
+                                    o.out_features, o.in_features, plan=o._plan, out=self.proj_out)
+            cur = 1 - cur
+            ops.bf16x_gemv_prenormed(R[cur], lay.mlp_norm, cfg.eps, self.slots, self.n_slots_o, g._sign, g._mant,
+                                     g._delta, g._emax, g.out_features, g.in_features, plan=g._plan, swiglu=True,
+                                     out=self.act[0])
+            ops.bf16x_gemv_residual(self.act[0], R[cur], R[1 - cur], self.slots, d._sign, d._mant, d._delta, d._emax,
+                                    d.out_features, d.in_features, plan=d._plan, out=self.proj_out)
+            cur = 1 - cur
+        return R[cur]
 
     # one pass over the stack for `T` tokens starting at position pos[0]
     def _layers(self, T: int, pos: torch.Tensor, ids: torch.Tensor):
@@ -445,6 +504,12 @@ class LlamaRunner:
         if self.fused_norm:
             down, res = self._decode_fused(self.state, self.token)
             self._head(down, res)
+            return
+        if self.res_norm:
+            h = self._decode_resnorm(self.state, self.token)
+            rmsnorm(h, self.model.norm, self.normed, eps=self.cfg.eps)
+            self.logits = self.model.lm_head(self.normed[0])
+            greedy(self.logits, self.token, self.state, self.history)
             return
         down = self._layers(1, self.state, self.token)
         self._head(down, self.residual[0])

@@ -225,6 +225,73 @@ def bf16x_gemv_norm(x, residual_in, norm_weight, residual_out, eps, sign, mant, 
     return y
 
 
+def gemv_residual_slots(out_f, in_f) -> int:
+    """Number of fp32 slots bf16x_gemv_residual writes for this shape."""
+    n = int(_lib.lib().bf16x_gemv_residual_slots(int(out_f), int(in_f)))
+    if n < 0:
+        raise _lib.Bf16xError(_lib.ESHAPE, "bf16x_gemv_residual_slots")
+    return n
+
+
+def bf16x_gemv_residual(x, residual_in, residual_out, slots, sign, mant, delta, emax, out_f, in_f,
+                        plan: Bf16xPlan | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """y = W . x, then h = bf16(y + residual_in) to residual_out and the sum of
+    h^2 per workgroup to `slots` (fp32, gemv_residual_slots(out_f, in_f)
+    entries), for a following bf16x_gemv_prenormed (include/bf16x_llama.h)."""
+    s, m, d, e = _streams(sign, mant, delta, emax)
+    out_f, in_f = int(out_f), int(in_f)
+    xx = _on(_dev_tensor(x, "x", (torch.bfloat16,)).reshape(-1), s.device, "x")
+    if xx.numel() != in_f:
+        raise ValueError(f"x has {xx.numel()} elements, in_f = {in_f}")
+    ri = _out(residual_in, out_f, s.device, "residual_in")
+    ro = _out(residual_out, out_f, s.device, "residual_out")
+    if not isinstance(slots, torch.Tensor) or slots.dtype != torch.float32 or not slots.is_contiguous():
+        raise ValueError("slots must be a contiguous fp32 tensor")
+    _on(slots, s.device, "slots")
+    _plan_on(plan, s.device, out_f, in_f)
+    y = _out(out, out_f, s.device) if out is not None else torch.empty(out_f, dtype=torch.bfloat16, device=s.device)
+    mode = _lib.SATURATED if plan is None else _lib.EXACT
+    st = _lib.lib().bf16x_gemv_residual(xx.data_ptr(), ri.data_ptr(), ro.data_ptr(), slots.data_ptr(), slots.numel(),
+                                        s.data_ptr(), s.numel(), m.data_ptr(), m.numel(), d.data_ptr(), d.numel(),
+                                        e.data_ptr(), e.numel(), _lib.ptr(plan.tile_off) if plan else None,
+                                        _lib.ptr(plan.tile_ent) if plan else None,
+                                        _lib.ptr(plan.tile_sat) if plan else None, out_f, in_f, mode, y.data_ptr(),
+                                        _lib.stream_of(s.device))
+    _lib.check(st, "bf16x_gemv_residual")
+    return y
+
+
+def bf16x_gemv_prenormed(h, norm_weight, eps, slots, n_slots, sign, mant, delta, emax, out_f, in_f,
+                         plan: Bf16xPlan | None = None, swiglu: bool = False,
+                         out: torch.Tensor | None = None) -> torch.Tensor:
+    """GEMV of RMSNorm(h) * norm_weight with the sum of h^2 read from the
+    first n_slots entries of `slots` (a bf16x_gemv_residual launch's);
+    swiglu: the SwiGLU epilogue (out_f // 2 outputs)."""
+    s, m, d, e = _streams(sign, mant, delta, emax)
+    out_f, in_f = int(out_f), int(in_f)
+    hh = _on(_dev_tensor(h, "h", (torch.bfloat16,)).reshape(-1), s.device, "h")
+    nw = _on(_dev_tensor(norm_weight, "norm_weight", (torch.bfloat16,)).reshape(-1), s.device, "norm_weight")
+    for t, nm in ((hh, "h"), (nw, "norm_weight")):
+        if t.numel() != in_f:
+            raise ValueError(f"{nm} has {t.numel()} elements, in_f = {in_f}")
+    if not isinstance(slots, torch.Tensor) or slots.dtype != torch.float32 or not slots.is_contiguous() or \
+            slots.numel() < int(n_slots):
+        raise ValueError("slots must be a contiguous fp32 tensor of at least n_slots entries")
+    _on(slots, s.device, "slots")
+    _plan_on(plan, s.device, out_f, in_f)
+    n_out = out_f // 2 if swiglu else out_f
+    y = _out(out, n_out, s.device) if out is not None else torch.empty(n_out, dtype=torch.bfloat16, device=s.device)
+    mode = _lib.SATURATED if plan is None else _lib.EXACT
+    st = _lib.lib().bf16x_gemv_prenormed(hh.data_ptr(), nw.data_ptr(), float(eps), slots.data_ptr(), int(n_slots),
+                                         s.data_ptr(), s.numel(), m.data_ptr(), m.numel(), d.data_ptr(), d.numel(),
+                                         e.data_ptr(), e.numel(), _lib.ptr(plan.tile_off) if plan else None,
+                                         _lib.ptr(plan.tile_ent) if plan else None,
+                                         _lib.ptr(plan.tile_sat) if plan else None, out_f, in_f, mode,
+                                         1 if swiglu else 0, y.data_ptr(), _lib.stream_of(s.device))
+    _lib.check(st, "bf16x_gemv_prenormed")
+    return y
+
+
 def bf16x_fused_gemv(x, sign, mant, delta, emax, olk, old, oloff, out_f, in_f, group=16, r=4, bk=256,
                      num_warps=2, *, plan: Bf16xPlan | None = None) -> torch.Tensor:
     """Fused decode+GEMV with the reference's signature (bf16x_fused.py:114).

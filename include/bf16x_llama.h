@@ -120,6 +120,34 @@ int bf16x_gemv_norm(const void* x, const uint16_t* residual_in, const uint16_t* 
                     const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
                     int64_t in_f, int32_t mode, int32_t epilogue, uint16_t* y, bf16x_stream_t stream);
 
+/* Fused decode+GEMV with the residual add of the layer it closes (the o and
+ * down projections): y = W . x as bf16x_gemv (bf16 x, in_f <= 16384), then
+ * h = bf16(y + residual_in) is stored to residual_out (residual_out may be
+ * residual_in; it must not alias x or y) and each workgroup b stores the sum
+ * of h^2 over its rows to slots[b], b < bf16x_gemv_residual_slots(out_f,
+ * in_f) (n_slots at least that; fp32, 4-byte aligned).  The next projection's
+ * RMSNorm then takes its sum of squares from the slots
+ * (bf16x_gemv_prenormed) instead of a launch of its own.  Folds the residual
+ * add and the statistics of the reference harness's post-attention /
+ * post-MLP RMSNorm into the projection before it. */
+int64_t bf16x_gemv_residual_slots(int64_t out_f, int64_t in_f);
+int bf16x_gemv_residual(const void* x, const uint16_t* residual_in, uint16_t* residual_out, float* slots,
+                        int64_t n_slots, const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                        const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                        const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
+                        int64_t in_f, int32_t mode, uint16_t* y, bf16x_stream_t stream);
+
+/* Fused decode+GEMV of RMSNorm(h) * norm_weight with the sum of h^2 given as
+ * n_slots partial sums (the slots of a bf16x_gemv_residual launch, added in
+ * slot order): the rows are multiplied with bf16(bf16(h * rsqrt(sum / in_f +
+ * eps)) * norm_weight).  epilogue 0 / 1 as bf16x_gemv_norm; h and norm_weight
+ * bf16, 4-byte aligned, in_f <= 4096. */
+int bf16x_gemv_prenormed(const void* h, const uint16_t* norm_weight, float eps, const float* slots, int64_t n_slots,
+                         const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                         const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                         const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
+                         int64_t in_f, int32_t mode, int32_t epilogue, uint16_t* y, bf16x_stream_t stream);
+
 /* Greedy step: token[0] = argmax(logits[0 .. vocab)) (the first maximum),
  * history[state[1]] = token[0] when state[1] < history_len, then state[1]++
  * and state[0]++.  logits 16-byte aligned. */

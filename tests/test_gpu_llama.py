@@ -378,6 +378,70 @@ def test_norm_in_gemv_decode_matches_prefill(small):
 
 
 @torch.no_grad()
+@pytest.mark.parametrize("out_f,in_f", [(512, 1024), (1000, 6144), (384, 14336)])
+def test_residual_and_prenormed_gemv(bx, out_f, in_f):
+    """bf16x_gemv_residual: y bit-identical to bf16x_gemv, residual_out =
+    bf16(y + residual_in) bit for bit, the slots add up to sum(h^2).
+    bf16x_gemv_prenormed with those slots: the GEMV of the RMSNorm of h within
+    the GEMV tolerance (its sum of squares is added in another order than the
+    standalone RMSNorm's, so the normalised input may differ by a rounding)."""
+    from bfloat16x_amd import ops
+    from oracle import dict_codec as dc
+    from tests.test_gpu_dict import bits_tensor, check_tol, to_dev
+    bits = dc.bench_weight_bits(out_f, in_f, seed=out_f + in_f)
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    plan = bx.build_plan_host(d, device=DEV)
+    streams = (g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"])
+    x = rnd(in_f, 1).to(DEV)
+    res = rnd(out_f, 2).to(DEV)
+    y = bx.bf16x_gemv(x, *streams, out_f, in_f, plan=plan)
+    n = ops.gemv_residual_slots(out_f, in_f)
+    slots = torch.full((n + 3,), float("nan"), dtype=torch.float32, device=DEV)
+    ro = torch.empty(out_f, dtype=torch.bfloat16, device=DEV)
+    yr = ops.bf16x_gemv_residual(x, res, ro, slots, *streams, out_f, in_f, plan=plan)
+    assert torch.equal(yr, y)
+    h = (y.float() + res.float()).to(torch.bfloat16)
+    assert torch.equal(ro, h)
+    ss = float((h.double() ** 2).sum())
+    assert abs(float(slots[:n].double().sum()) - ss) <= 1e-5 * ss
+    assert torch.isnan(slots[n:]).all()                           # only the launch's own slots are written
+    # the next projection: RMSNorm(h) * w as its input
+    if out_f <= 4096 and out_f % 32 == 0:
+        nxt = dc.bench_weight_bits(256, out_f, seed=7)
+        d2 = bx.bf16x_quantize(bits_tensor(nxt))
+        g2 = to_dev(d2)
+        p2 = bx.build_plan_host(d2, device=DEV)
+        w = (1.0 + 0.1 * rnd(out_f, 3).float()).to(torch.bfloat16).to(DEV)
+        normed = torch.empty(out_f, dtype=torch.bfloat16, device=DEV)
+        llama.rmsnorm(h, w, normed, eps=1e-5)
+        s2 = (g2["sign_packed"], g2["mant_packed"], g2["delta_packed"], g2["emax"])
+        ref = bx.bf16x_gemv(normed, *s2, 256, out_f, plan=p2)
+        got = ops.bf16x_gemv_prenormed(h, w, 1e-5, slots, n, *s2, 256, out_f, plan=p2)
+        check_tol(got.float().cpu().numpy(), ref.float().cpu().numpy().astype(np.float64))
+
+
+@torch.no_grad()
+def test_residual_norm_decode_matches_prefill_and_unfused(small):
+    """The default BF16X decode step (residual adds and RMSNorm statistics
+    carried by the o / down GEMVs, bf16x_gemv_residual / _prenormed) against
+    a prefill over the same tokens and against the decode with standalone
+    RMSNorm launches."""
+    _, mx, _, ids = small
+    r = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32)
+    assert r.res_norm
+    toks = r.generate(ids.to(DEV), 6, graph=False)
+    last = r.logits.float().cpu().numpy()
+    r2 = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32)
+    r2.prefill(torch.cat([ids, torch.tensor(toks[:-1])]).to(DEV))
+    assert norm_rel(last, r2.logits.float().cpu().numpy()) < 1e-2
+    r3 = llama.LlamaRunner(mx, max_len=64, max_new=8, max_prompt=32, residual_norm=False)
+    assert not r3.res_norm and not r3.fused_norm
+    r3.generate(ids.to(DEV), 6, graph=False)
+    assert norm_rel(last, r3.logits.float().cpu().numpy()) < 1e-2
+
+
+@torch.no_grad()
 def test_graph_decode_matches_eager_over_replays(small):
     _, mx, _, ids = small
     r = llama.LlamaRunner(mx, max_len=64, max_new=12, max_prompt=32)
