@@ -57,7 +57,9 @@ def test_dequantize_blocks_api(bx):
     assert dev.is_cuda and np.array_equal(dev.cpu().numpy().view(np.uint32), back.view(np.uint32))
 
 
-@pytest.mark.parametrize("shape", [(256, 4096), (96, 28672), (1000, 1024)])
+# (4100, 4224): the long-row GEMV with a partial last pass (132 blocks per
+# row), two rows per wave and a ragged last workgroup
+@pytest.mark.parametrize("shape", [(256, 4096), (96, 28672), (1000, 1024), (4100, 4224)])
 def test_gemv_and_gemm(bx, shape):
     out_f, in_f = shape
     w = gc.student_t_weights(out_f, in_f, seed=2)

@@ -32,8 +32,10 @@ def dense_overflow(rows, cols, seed):
     return w
 
 
+# ("dense", (4100, 4224)): the long-row GEMV (3 passes of 64 blocks), two rows
+# per wave, rows 1 and 2 with more entries than the read-ahead batches
 CASES = [("selftest", (256, 512)), ("selftest", (300, 576)), ("dense", (8, 4096)), ("dense", (5, 8192)),
-         ("selftest", (64, 2080))]
+         ("selftest", (64, 2080)), ("dense", (4100, 4224))]
 
 
 def weights(kind, shape, seed):

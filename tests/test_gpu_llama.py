@@ -378,8 +378,9 @@ def test_norm_in_gemv_decode_matches_prefill(small):
 
 
 @torch.no_grad()
-@pytest.mark.parametrize("out_f,in_f", [(512, 1024), (1000, 6144), (384, 14336)])
-def test_residual_and_prenormed_gemv(bx, out_f, in_f):
+@pytest.mark.parametrize("out_f,in_f,dense", [(512, 1024, False), (1000, 6144, False), (384, 14336, False),
+                                              (4100, 6144, True)])
+def test_residual_and_prenormed_gemv(bx, out_f, in_f, dense):
     """bf16x_gemv_residual: y bit-identical to bf16x_gemv, residual_out =
     bf16(y + residual_in) bit for bit, the slots add up to sum(h^2).
     bf16x_gemv_prenormed with those slots: the GEMV of the RMSNorm of h within
@@ -389,6 +390,9 @@ def test_residual_and_prenormed_gemv(bx, out_f, in_f):
     from oracle import dict_codec as dc
     from tests.test_gpu_dict import bits_tensor, check_tol, to_dev
     bits = dc.bench_weight_bits(out_f, in_f, seed=out_f + in_f)
+    if dense:                  # 30 % tiny elements: every row has more entries than the read-ahead batches
+        tiny = np.random.default_rng(5).random(bits.shape) < 0.3
+        bits[tiny] = (bits[tiny] & 0x807F) | 0x0080
     d = bx.bf16x_quantize(bits_tensor(bits))
     g = to_dev(d)
     plan = bx.build_plan_host(d, device=DEV)
