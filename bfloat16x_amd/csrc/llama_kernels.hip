@@ -647,12 +647,22 @@ extern "C" int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const
 // is processed.  At the end the 8 waves' states are combined in LDS in wave
 // order.  The new row (position p) is rotated and appended as in
 // rope_kv_kernel and read from LDS.
+// Per-head variant (PH, W = 16 waves, NB blocks of 256 keys): one workgroup
+// per QUERY head (the group's K and V rows are read by its G workgroups, from
+// L2), and the rows of all NB blocks are requested at entry, before the
+// position is known (clamped into the cache; a row at or past the position
+// is replaced by the new row from LDS, as above), so a context of up to
+// 16 W NB keys costs one memory round trip instead of a chain of blocks or
+// the split kernel's partials and counter.  The first workgroup of a group
+// appends the new row.
 constexpr int kDec1MaxLen = 256;
 constexpr int kDec1Waves = 8;
-constexpr int kDec1Block = 16 * kDec1Waves;    // keys per block
+constexpr int kDecHWaves = 16;
+constexpr int kDecHBlocks = 3;
+constexpr int kDecHMaxLen = 16 * kDecHWaves * kDecHBlocks;   // 768
 
-template <int G>
-__global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uint16_t* __restrict__ qkv,
+template <int G, int W = kDec1Waves, bool PH = false, int NB = 0>
+__global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __restrict__ qkv,
                                                             const int32_t* __restrict__ pos,
                                                             const float* __restrict__ cs, int H, int KV,
                                                             int max_len, float scale, uint16_t* __restrict__ kc,
@@ -660,20 +670,23 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
   __shared__ uint32_t qs2[G][64];          // rotated q as bf16 pairs (dims 2i, 2i+1)
   __shared__ uint32_t kp2[64];             // the new key, likewise
   __shared__ float vp[128];
-  __shared__ float ps[kDec1Waves][G][16];  // per wave: the scores of its 16 keys of a block
-  __shared__ float pw[kDec1Waves][G][16];  // per wave: their probabilities
-  __shared__ float wm[kDec1Waves][G], wl[kDec1Waves][G];   // per wave: running max and sum
-  __shared__ float wacc[kDec1Waves][G][128];                // per wave: unnormalised output
-  const int g = blockIdx.x;
+  constexpr int kBlock = 16 * W;           // keys per block
+  __shared__ float ps[W][G][16];           // per wave: the scores of its 16 keys of a block
+  __shared__ float pw[W][G][16];           // per wave: their probabilities
+  __shared__ float wm[W][G], wl[W][G];     // per wave: running max and sum
+  __shared__ float wacc[W][G][128];        // per wave: unnormalised output
+  // PH: workgroup = query head hq of KV head g (G == 1); else workgroup = KV head g, query heads g G + h
+  const int gq = H / KV;
+  const int g = PH ? (int)blockIdx.x / gq : (int)blockIdx.x;
+  const int hq0 = PH ? (int)blockIdx.x : g * G;
+  const bool writer = !PH || (int)blockIdx.x % gq == 0;   // appends the new K / V row
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = lane >> 2, q4 = lane & 3;
-  const int p = pos[0];
-  const bool cur = p >= 0 && p < max_len;                        // the new row fits in the cache
-  const int n_old = p < 0 ? 0 : (p > max_len ? max_len : p);     // cached keys 0 .. n_old - 1
-  const int n = n_old + (cur ? 1 : 0);
-  const int nb = (n + kDec1Block - 1) / kDec1Block;
-  const int jmax = n_old > 0 ? n_old - 1 : 0;                    // loads are clamped to a cached row
+  // NB > 0: the entry loads are issued before the position is read,
+  // clamped into the cache instead of to the cached rows
+  const int p = NB > 0 ? 0 : pos[0];
+  const int jmax_entry = max_len - 1;
   // this KV head's cache rows through buffer descriptors: 32-bit offsets, the
   // key index of a V load uniform (a scalar offset)
   const uint64_t head_bytes = (uint64_t)max_len * 256;
@@ -681,8 +694,9 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
       __builtin_amdgcn_make_buffer_rsrc((void*)(kc + (int64_t)g * max_len * 128), (short)0, (int)head_bytes, 0x00020000);
   const __amdgpu_buffer_rsrc_t rv =
       __builtin_amdgcn_make_buffer_rsrc((void*)(vc + (int64_t)g * max_len * 128), (short)0, (int)head_bytes, 0x00020000);
+  int jmax = jmax_entry;
   auto load_k = [&](int b, u32x4 (&kr)[4]) {
-    const int j = min(kDec1Block * b + 16 * w + kg, jmax);
+    const int j = min(kBlock * b + 16 * w + kg, jmax);
     const int off = j * 256 + 64 * q4;
 #pragma unroll
     for (int c = 0; c < 4; ++c) kr[c] = __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16 * c, 0, 0);
@@ -690,20 +704,36 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
   auto load_v = [&](int b, uint32_t (&vr)[16]) {
 #pragma unroll
     for (int u = 0; u < 16; ++u)
-      vr[u] = __builtin_amdgcn_raw_buffer_load_b32(rv, 4 * lane, min(kDec1Block * b + 16 * w + u, jmax) * 256, 0);
+      vr[u] = __builtin_amdgcn_raw_buffer_load_b32(rv, 4 * lane, min(kBlock * b + 16 * w + u, jmax) * 256, 0);
   };
-  u32x4 kA[4], kB[4];
-  uint32_t vA[16], vB[16];
-  load_k(0, kA);
-  load_v(0, vA);
-  load_k(1, kB);
-  load_v(1, vB);
+  constexpr int NR = NB > 0 ? NB : 2;      // blocks of K / V rows in registers
+  u32x4 kR[NR][4];
+  uint32_t vR[NR][16];
+  if constexpr (NB > 0) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      load_k(b, kR[b]);
+      load_v(b, vR[b]);
+    }
+  }
+  const int pp = NB > 0 ? pos[0] : p;
+  const bool cur = pp >= 0 && pp < max_len;                      // the new row fits in the cache
+  const int n_old = pp < 0 ? 0 : (pp > max_len ? max_len : pp);  // cached keys 0 .. n_old - 1
+  const int n = n_old + (cur ? 1 : 0);
+  const int nb = (n + kBlock - 1) / kBlock;
+  jmax = n_old > 0 ? n_old - 1 : 0;                              // later loads: clamped to a cached row
+  if constexpr (NB == 0) {
+    load_k(0, kR[0]);
+    load_v(0, vR[0]);
+    load_k(1, kR[1]);
+    load_v(1, vR[1]);
+  }
   // rotary embedding of the q heads and the new key, KV append
   {
-    const int pc = p < 0 ? 0 : (p >= max_len ? max_len - 1 : p);
-    for (int hh = w; hh < G + 2; hh += kDec1Waves) {
+    const int pc = pp < 0 ? 0 : (pp >= max_len ? max_len - 1 : pp);
+    for (int hh = w; hh < G + 2; hh += W) {
       const float c = cs[((int64_t)pc * 64 + lane) * 2], sn = cs[((int64_t)pc * 64 + lane) * 2 + 1];
-      const int head = hh < G ? g * G + hh : (hh == G ? H + g : H + KV + g);
+      const int head = hh < G ? hq0 + hh : (hh == G ? H + g : H + KV + g);
       const uint16_t* src = qkv + (int64_t)head * 128;
       const uint16_t a16 = src[lane], b16 = src[lane + 64];
       if (hh <= G) {
@@ -713,8 +743,8 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
         d16[lane] = (uint16_t)ra;
         d16[lane + 64] = (uint16_t)rb;
         if (hh == G) {
-          if (cur) {
-            uint16_t* dst = kc + ((int64_t)g * max_len + p) * 128;
+          if (cur && writer) {
+            uint16_t* dst = kc + ((int64_t)g * max_len + pp) * 128;
             dst[lane] = (uint16_t)ra;
             dst[lane + 64] = (uint16_t)rb;
           }
@@ -722,8 +752,8 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
       } else {
         vp[lane] = bfv(a16);
         vp[lane + 64] = bfv(b16);
-        if (cur) {
-          uint16_t* dst = vc + ((int64_t)g * max_len + p) * 128;
+        if (cur && writer) {
+          uint16_t* dst = vc + ((int64_t)g * max_len + pp) * 128;
           dst[lane] = a16;
           dst[lane + 64] = b16;
         }
@@ -742,7 +772,7 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
   auto block = [&](int b, u32x4 (&kr)[4], uint32_t (&vr)[16]) {
     // scores of key j: four lanes, 32 dims (16 bf16 pairs) each, exact
     // products in fp32 (v_dot2), scaled after the sum
-    const int j = kDec1Block * b + 16 * w + kg;
+    const int j = kBlock * b + 16 * w + kg;
     uint32_t kw[16];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -806,7 +836,7 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
     float v0[16], v1[16];
 #pragma unroll
     for (int u = 0; u < 16; ++u) {
-      const bool nw = kDec1Block * b + 16 * w + u >= n_old;     // uniform
+      const bool nw = kBlock * b + 16 * w + u >= n_old;         // uniform
       v0[u] = nw ? vn0 : bf16lo_to_f32(vr[u]);
       v1[u] = nw ? vn1 : bf16hi_to_f32(vr[u]);
     }
@@ -827,16 +857,24 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
       l[h] += lsum;
     }
     __builtin_amdgcn_wave_barrier();
-    // the next block but one into these registers
-    load_k(b + 2, kr);
-    load_v(b + 2, vr);
+    if constexpr (NB == 0) {
+      // the next block but one into these registers
+      load_k(b + 2, kr);
+      load_v(b + 2, vr);
+    }
   };
-  int b = 0;
-  for (; b + 1 < nb; b += 2) {
-    block(b, kA, vA);
-    block(b + 1, kB, vB);
+  if constexpr (NB > 0) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      if (b < nb) block(b, kR[b], vR[b]);
+  } else {
+    int b = 0;
+    for (; b + 1 < nb; b += 2) {
+      block(b, kR[0], vR[0]);
+      block(b + 1, kR[1], vR[1]);
+    }
+    if (b < nb) block(b, kR[0], vR[0]);
   }
-  if (b < nb) block(b, kA, vA);
 
   // combine the waves in wave order
   if (lane == 0) {
@@ -852,19 +890,19 @@ __global__ __launch_bounds__(64 * kDec1Waves) void attn_decode1_kernel(const uin
     wacc[w][h][2 * lane + 1] = acc[h][1];
   }
   __syncthreads();
-  for (int e = tid; e < G * 128; e += 64 * kDec1Waves) {
+  for (int e = tid; e < G * 128; e += 64 * W) {
     const int h = e >> 7, d = e & 127;
     float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < kDec1Waves; ++k) M = fmaxf(M, wm[k][h]);
+    for (int k = 0; k < W; ++k) M = fmaxf(M, wm[k][h]);
     float L = 0.f, o = 0.f;
 #pragma unroll
-    for (int k = 0; k < kDec1Waves; ++k) {
+    for (int k = 0; k < W; ++k) {
       const float f = wm[k][h] == -INFINITY ? 0.f : __expf(wm[k][h] - M);
       L = fmaf(wl[k][h], f, L);
       o = fmaf(wacc[k][h][d], f, o);
     }
-    out[(int64_t)(g * G + h) * 128 + d] = (uint16_t)f32_to_bf16_rne(L > 0.f ? o / L : 0.f);
+    out[(int64_t)(hq0 + h) * 128 + d] = (uint16_t)f32_to_bf16_rne(L > 0.f ? o / L : 0.f);
   }
 }
 
@@ -918,6 +956,12 @@ extern "C" int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, c
       default: BF16X_DEC1(8); break;
     }
 #undef BF16X_DEC1
+    return launch_status();
+  }
+  if (max_len <= kDecHMaxLen && !getenv("BF16X_ATTN_SPLIT")) {
+    hipLaunchKernelGGL((attn_decode1_kernel<1, kDecHWaves, true, kDecHBlocks>), dim3((unsigned)n_heads),
+                       dim3(64 * kDecHWaves), 0, st, qkv, pos, cos_sin, (int)n_heads, (int)n_kv_heads, (int)max_len,
+                       scale, k_cache, v_cache, out);
     return launch_status();
   }
   const int S = host_dec_splits(max_len);

@@ -67,8 +67,9 @@ int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* 
 
 /* One decode token (at position *pos) through rotary embedding, KV append and
  * attention in one launch: bf16x_rope_kv followed by bf16x_attention with
- * tokens = 1.  Up to max_len = 256 one workgroup per KV head takes all keys
- * (the workspace is not touched); above, the keys are split into ranges
+ * tokens = 1.  Up to max_len = 256 one workgroup per KV head takes all keys,
+ * up to max_len = 768 one workgroup per query head (all K / V rows requested
+ * at once), in both cases without touching the workspace; above, the keys are split into ranges
  * served by separate workgroups whose partial results meet in `workspace`
  * (bf16x_attention_decode_workspace bytes, 16-byte aligned, required in both
  * cases).  The workspace starts with one counter per KV head

@@ -158,13 +158,15 @@ def test_attention(bx, T, pos, L):
 @pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("H,KV,pos,L", [(4, 4, 0, 16), (8, 4, 5, 64), (32, 8, 300, 640), (32, 8, 639, 640),
                                         (16, 2, 100, 640), (8, 1, 31, 48), (32, 8, 3000, 4096),
-                                        (64, 8, 511, 1024), (32, 8, 1, 640), (32, 8, 199, 200)])
+                                        (64, 8, 511, 1024), (32, 8, 1, 640), (32, 8, 199, 200),
+                                        (32, 8, 767, 768), (64, 8, 700, 768), (8, 2, 400, 769), (32, 8, 257, 260)])
 def test_attention_decode_matches_two_launch_path(bx, H, KV, pos, L, split, monkeypatch):
     """The fused one-token kernel against rope_kv + attention on the same
     inputs: the same cache rows and outputs (one bf16 rounding apart at
     most), and the fp32 reference.  Contexts up to 256 keys run the
-    one-workgroup-per-KV-head kernel unless BF16X_ATTN_SPLIT selects the
-    split kernel (which longer contexts always use)."""
+    one-workgroup-per-KV-head kernel, up to 768 the one-workgroup-per-query-
+    head kernel, unless BF16X_ATTN_SPLIT selects the split kernel (which
+    longer contexts always use)."""
     if split:
         monkeypatch.setenv("BF16X_ATTN_SPLIT", "1")
     assert llama.attention_decode_supported(H, KV, L)
