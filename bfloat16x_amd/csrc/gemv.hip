@@ -874,9 +874,12 @@ int launch_gemv_g1(const void* x, const uint32_t* sign, const uint32_t* mant, co
   int iters = EPI == 1 ? 2 : (groups >= 1024 ? 2 : 1);
   if (XM != 0) {
     // every workgroup normalises x in its prologue (with its own pass over
-    // x): enough rows per workgroup that the grid fits one round of resident
-    // workgroups (4 per CU)
-    const int64_t slots = 1024;
+    // x): at least groups / 2048 row groups per workgroup (BF16X_GEMV_XM_SLOTS
+    // overrides 2048).  Measured in the Llama decode step (gate_up, 7168
+    // groups): 2048 -> 1792 workgroups, 7 per CU, 334.8 tok/s; 1024 -> 896,
+    // 3.5 per CU, 327.5; 512 -> 512, 333.0; 4096 -> 3584, 309.6
+    int64_t slots = 2048;
+    if (const char* e = getenv("BF16X_GEMV_XM_SLOTS")) slots = std::max<int64_t>(1, atoll(e));
     iters = std::max<int64_t>(iters, (groups + slots - 1) / slots);
     if (EPI == 1) iters += iters & 1;
   }
