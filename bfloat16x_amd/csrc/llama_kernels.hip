@@ -555,13 +555,29 @@ __global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t* __restrict
   int bi = 0x7FFFFFFF;
   const int tid = threadIdx.x;
   const int full = V & ~7;
-  for (int i = tid * 8; i < full; i += 1024 * 8) {
-    const u32x4 v = *(const u32x4*)(logits + i);
-    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  // 16 chunks of 8 logits per thread requested before any is compared (a
+  // 128256-entry vocabulary is one batch: one memory round trip instead of
+  // sixteen), then compared in index order
+  constexpr int kBatch = 16;
+  for (int base = tid * 8; base < full; base += 1024 * 8 * kBatch) {
+    u32x4 v[kBatch];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      better(bv, bi, bf16lo_to_f32(w[k]), i + 2 * k);
-      better(bv, bi, bf16hi_to_f32(w[k]), i + 2 * k + 1);
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = base + u * 1024 * 8;
+      v[u] = i < full ? *(const u32x4*)(logits + i) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int i = base + u * 1024 * 8;
+      if (i < full) {
+        const u32x4 vu = v[u];
+        const uint32_t w[4] = {vu.x, vu.y, vu.z, vu.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          better(bv, bi, bf16lo_to_f32(w[k]), i + 2 * k);
+          better(bv, bi, bf16hi_to_f32(w[k]), i + 2 * k + 1);
+        }
+      }
     }
   }
   if (tid < V - full) better(bv, bi, bfv(logits[full + tid]), full + tid);

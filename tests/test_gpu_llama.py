@@ -236,7 +236,7 @@ def test_gemv_swiglu_matches_unfused(bx, F, in_f, mode):
 
 
 @torch.no_grad()
-@pytest.mark.parametrize("V", [1000, 1003, 128256])
+@pytest.mark.parametrize("V", [1000, 1003, 128256, 140003])
 def test_greedy(bx, V):
     logits = rnd(V, 12)
     logits[V // 3] = 9.0
