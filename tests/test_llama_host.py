@@ -64,6 +64,11 @@ def test_entry_points_validate_before_launch():
     # decode attention: unsupported head ratio, workspace too small
     assert _call("bf16x_attention_decode_lds", 24, 8, 640) == -1
     assert _call("bf16x_attention_decode_workspace", 32, 8, 640) > 0
+    # every cache length the three decode kernels serve (one workgroup per kv
+    # head, per query head, split) has a workspace size and a workgroup-memory size
+    for L in (1, 256, 257, 768, 769, 4096, 16384):
+        assert _call("bf16x_attention_decode_lds", 32, 8, L) > 0
+        assert _call("bf16x_attention_decode_workspace", 32, 8, L) > 0
     assert _call("bf16x_attention_decode", p, p, p, 24, 8, 128, 640, 0.1, p, p, p, 1 << 20, p, None) == _lib.ESHAPE
     assert _call("bf16x_attention_decode", p, p, p, 32, 8, 128, 640, 0.1, p, p, p, 64, p, None) == _lib.ECAPACITY
     # silu_mul: ffn % 8, layout code
