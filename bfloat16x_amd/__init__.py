@@ -16,7 +16,7 @@ Call surface (mirrors the reference dfytensor/bfloat16x):
 All GPU work runs in the HIP library libbf16x_hip.so through its C ABI
 (include/bf16x_hip.h, include/bf16x_llama.h).
 """
-from ._lib import Bf16xError, version
+from ._lib import Bf16xError, tuning, version
 from .codec import Bf16xPlan, bf16x_quantize, build_plan_host, stream_words
 from . import disk, gguf, llama
 from .disk import Bf16xStreamLinear, pack_model_to_disk, replace_linears_from_packed
@@ -29,5 +29,5 @@ __all__ = [
     "Bf16xError", "Bf16xPlan", "bf16x_decode", "bf16x_decode_triton", "bf16x_fused_gemm", "bf16x_fused_gemv",
     "bf16x_gemm", "bf16x_gemv",
     "bf16x_quantize", "build_plan_host", "gguf", "stream_words", "version",
-    "disk", "llama", "Bf16xStreamLinear", "pack_model_to_disk", "replace_linears_from_packed",
+    "disk", "llama", "Bf16xStreamLinear", "pack_model_to_disk", "replace_linears_from_packed", "tuning",
 ]

@@ -77,6 +77,16 @@ PROTOTYPES = {
     "bf16x_gemv_prenormed": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
                                             _P, _c_i64, _P, _P, _P, _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
     "bf16x_greedy": (ctypes.c_int, [_P, _c_i64, _P, _P, _P, _c_i64, _P]),
+    # kernel-choice overrides (include/bf16x_hip.h)
+    "bf16x_set_tuning": (ctypes.c_int, [_c_i32, _c_i64]),
+    "bf16x_get_tuning": (_c_i64, [_c_i32]),
+}
+
+# keys of bf16x_set_tuning (BF16X_TUNE_* in include/bf16x_hip.h)
+TUNE_KEYS = {
+    "gemm_skinny2_max": 0, "gemm_skinny_max": 1, "gemm_bm": 2, "gemm_split": 3, "gemm_ws_min_rows": 4,
+    "gemm_ws_split": 5, "skinny_waves": 6, "skinny2_kq": 7, "skinny2_split": 8, "gemv_iters": 9, "gemv_g": 10,
+    "gemv_long": 11, "gemv_xm_slots": 12, "gguf_long": 13, "gguf_iters": 14, "attn_split": 15,
 }
 
 _LIB = None
@@ -130,3 +140,30 @@ def stream_of(device: torch.device):
 
 def version() -> str:
     return lib().bf16x_version().decode()
+
+
+class tuning:
+    """Context manager over bf16x_set_tuning: forces kernel choices for the
+    duration of a `with` block (a test and sweep hook), then restores the
+    previous values.  tuning(gemm_ws_min_rows=1 << 30) keeps every GEMM off
+    the wave-specialised kernel, for instance."""
+
+    def __init__(self, **overrides: int):
+        unknown = set(overrides) - set(TUNE_KEYS)
+        if unknown:
+            raise KeyError(f"unknown tuning keys {sorted(unknown)}")
+        self.overrides = {TUNE_KEYS[k]: int(v) for k, v in overrides.items()}
+        self.saved: dict[int, int] = {}
+
+    def __enter__(self):
+        L = lib()
+        for k, v in self.overrides.items():
+            self.saved[k] = int(L.bf16x_get_tuning(k))
+            check(L.bf16x_set_tuning(k, v), "bf16x_set_tuning")
+        return self
+
+    def __exit__(self, *exc):
+        L = lib()
+        for k, v in self.saved.items():
+            L.bf16x_set_tuning(k, v)
+        return False

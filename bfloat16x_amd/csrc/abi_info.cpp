@@ -1,4 +1,6 @@
-// Version and status strings of the C ABI.
+// Version and status strings of the C ABI, and the kernel-choice overrides.
+#include <atomic>
+
 #include "../../include/bf16x_hip.h"
 
 extern "C" const char* bf16x_version(void) { return "bf16x-hip 0.1.0 gfx950"; }
@@ -16,3 +18,20 @@ extern "C" const char* bf16x_status_string(int status) {
     default: return status > 0 ? "HIP runtime error" : "unknown status";
   }
 }
+
+// Overrides stored as value + 1 so the zero-initialised table means
+// "automatic" for every key.
+static std::atomic<int64_t> g_tuning[BF16X_TUNE_COUNT];
+
+int64_t bf16x_tuning_value(int key) {
+  if (key < 0 || key >= BF16X_TUNE_COUNT) return -1;
+  return g_tuning[key].load(std::memory_order_relaxed) - 1;
+}
+
+extern "C" int bf16x_set_tuning(int32_t key, int64_t value) {
+  if (key < 0 || key >= BF16X_TUNE_COUNT) return BF16X_EARG;
+  g_tuning[key].store(value < 0 ? 0 : value + 1, std::memory_order_relaxed);
+  return BF16X_OK;
+}
+
+extern "C" int64_t bf16x_get_tuning(int32_t key) { return bf16x_tuning_value(key); }

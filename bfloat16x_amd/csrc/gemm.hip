@@ -460,6 +460,13 @@ extern "C" int bf16x_kplan_build(const uint32_t* tile_off, const uint32_t* tile_
   return launch_status();
 }
 
+// wave-specialised kernel (gemm_ws.hip): M >= ws_rows()
+int64_t bf16x_gemm_ws_workspace(int64_t M, int64_t out_f, int64_t in_f);
+int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m, const uint32_t* d,
+                         const uint16_t* e, const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f,
+                         int64_t in_f, bool exact, bool yf32, void* y, void* workspace, int64_t workspace_bytes,
+                         hipStream_t st);
+
 // few-row kernel (gemm_skinny.hip): M <= skinny_rows()
 int bf16x_gemm_skinny_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m, const uint32_t* d,
                              const uint16_t* e, const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f,
@@ -477,19 +484,29 @@ namespace {
 // Largest M served by the 16x16x32-MFMA few-row kernel (at most 64).
 int64_t skinny2_rows() {
   int64_t r = 64;
-  if (const char* e = getenv("BF16X_GEMM_SKINNY2_MAX")) r = atoll(e);
+  if (const int64_t t = tuning(BF16X_TUNE_GEMM_SKINNY2_MAX); t >= 0) r = t;
   return r < 0 ? 0 : (r > 64 ? 64 : r);
 }
 
 bool use_skinny2(int64_t M, int64_t in_f) { return M <= skinny2_rows() && in_f % 128 == 0; }
 
+// Smallest M served by the wave-specialised kernel (256-row tiles).
+int64_t ws_rows() {
+  const int64_t t = tuning(BF16X_TUNE_GEMM_WS_MIN_ROWS);
+  return t >= 0 ? t : 192;
+}
+
+
 // Largest M served by the few-row kernel (at most 128, its column-block
 // limit; measured faster than the tiled kernel up to 32 rows).
 int64_t skinny_rows() {
   int64_t r = 32;
-  if (const char* e = getenv("BF16X_GEMM_SKINNY_MAX")) r = atoll(e);
+  if (const int64_t t = tuning(BF16X_TUNE_GEMM_SKINNY_MAX); t >= 0) r = t;
   return r < 0 ? 0 : (r > 128 ? 128 : r);
 }
+
+// M >= ws_rows() and past both few-row kernels
+bool use_ws(int64_t M, int64_t in_f) { return M >= ws_rows() && !use_skinny2(M, in_f) && M > skinny_rows(); }
 
 struct GemmShape {
   int bm;        // rows of x per tile
@@ -505,7 +522,7 @@ struct GemmShape {
 GemmShape gemm_shape(int64_t M, int64_t out_f, int64_t in_f) {
   GemmShape g;
   g.bm = M <= 32 ? 32 : M <= 64 ? 64 : M <= 128 ? 128 : 256;
-  if (const char* e = getenv("BF16X_GEMM_BM")) g.bm = atoi(e);
+  if (const int64_t t = tuning(BF16X_TUNE_GEMM_BM); t >= 0) g.bm = (int)t;
   const int64_t S = in_f / kBK;
   const int64_t tiles = ((M + g.bm - 1) / g.bm) * ((out_f + kBN - 1) / kBN);
   const int64_t slots = 256 * (g.bm <= 128 ? 2 : 1);   // resident blocks (LDS: 66 / 80 / 112 KB)
@@ -516,7 +533,7 @@ GemmShape gemm_shape(int64_t M, int64_t out_f, int64_t in_f) {
     const double cost = (double)((tiles * ks + slots - 1) / slots) * sps * (1.0 + 0.15 * (ks - 1));
     if (cost < best_cost - 1e-9) { best_cost = cost; best = (int)ks; }
   }
-  if (const char* e = getenv("BF16X_GEMM_SPLIT")) best = atoi(e);
+  if (const int64_t t = tuning(BF16X_TUNE_GEMM_SPLIT); t >= 0) best = (int)std::min<int64_t>(t, S);
   if (best < 1) best = 1;
   g.sps = (int)((S + best - 1) / best);
   g.nsplit = (int)((S + g.sps - 1) / g.sps);
@@ -529,6 +546,7 @@ extern "C" int64_t bf16x_gemm_workspace(int64_t M, int64_t out_f, int64_t in_f) 
   if (M <= 0 || out_f <= 0 || in_f < kBK) return 0;
   if (use_skinny2(M, in_f)) return bf16x_gemm_skinny2_workspace(M, out_f, in_f);
   if (M <= skinny_rows()) return 0;
+  if (use_ws(M, in_f)) return bf16x_gemm_ws_workspace(M, out_f, in_f);
   const GemmShape g = gemm_shape(M, out_f, in_f);
   return g.nsplit > 1 ? (int64_t)g.nsplit * M * out_f * 4 : 0;
 }
@@ -561,6 +579,12 @@ extern "C" int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M, const int32
     rc = bf16x_gemm_skinny_launch((const uint16_t*)x, M, (const uint32_t*)sign, (const uint32_t*)mant,
                                   (const uint32_t*)delta, (const uint16_t*)emax, kp_off, kp_ent, out_f, in_f,
                                   mode == BF16X_EXACT, y_dtype == BF16X_F32, y, st);
+    return rc ? rc : launch_status();
+  }
+  if (use_ws(M, in_f)) {
+    rc = bf16x_gemm_ws_launch((const uint16_t*)x, M, (const uint32_t*)sign, (const uint32_t*)mant,
+                              (const uint32_t*)delta, (const uint16_t*)emax, kp_off, kp_ent, out_f, in_f,
+                              mode == BF16X_EXACT, y_dtype == BF16X_F32, y, workspace, workspace_bytes, st);
     return rc ? rc : launch_status();
   }
   const GemmShape g = gemm_shape(M, out_f, in_f);

@@ -285,7 +285,7 @@ int bf16x_gemm_skinny_launch(const uint16_t* x, int64_t M, const uint32_t* s, co
   if (G > INT32_MAX) return BF16X_ESHAPE;
   // waves per block (K split): enough resident waves to stream W
   int waves = G >= 512 ? 4 : (G >= 256 ? 8 : 16);
-  if (const char* env = getenv("BF16X_SKINNY_WAVES")) waves = atoi(env);
+  if (const int64_t t = tuning(BF16X_TUNE_SKINNY_WAVES); t > 0) waves = (int)t;
   const int nc = M <= 32 ? 1 : (M <= 64 ? 2 : 4);
   // register budget: 16 waves per block leave 128 VGPRs per lane (one column
   // block), 8 waves 256 (two); four column blocks run 4 waves per block

@@ -381,14 +381,12 @@ struct Split {
 // up to 32 rows (16 waves per workgroup), 2 above (8 waves: the x tile of 4
 // steps for 64 tokens would not fit beside the scratch, the tile of 2 steps
 // does; 64 rows at 14336 x 4096: 47 us against 55 us with one wave per
-// row group).  BF16X_SKINNY2_KQ=1 or 2 overrides.
+// row group).  The override BF16X_TUNE_SKINNY2_KQ = 1 or 2 replaces it.
 int nc_for(int64_t M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
 int kq_for(int64_t M) {
-  if (const char* e = getenv("BF16X_SKINNY2_KQ")) {
-    const int k = atoi(e);
-    if (k == 1) return 1;
-    if (k == 2) return 2;
-  }
+  const int64_t k = tuning(BF16X_TUNE_SKINNY2_KQ);
+  if (k == 1) return 1;
+  if (k == 2) return 2;
   return nc_for(M) <= 2 ? 4 : 2;
 }
 
@@ -438,7 +436,7 @@ Split skinny2_split(int64_t M, int64_t out_f, int64_t in_f, bool exact) {
   const int64_t kq = kq_for(M);
   int64_t ks = slots_for(M, exact) / tiles;
   ks = std::max<int64_t>(1, std::min<int64_t>(ks, S / (2 * kq)));
-  if (const char* e = getenv("BF16X_SKINNY2_SPLIT")) ks = std::max<int64_t>(1, std::min<int64_t>(atoll(e), S));
+  if (const int64_t t = tuning(BF16X_TUNE_SKINNY2_SPLIT); t > 0) ks = std::min<int64_t>(t, S);
   Split sp;
   int64_t sps = (S + ks - 1) / ks;
   sps = (sps + kq - 1) / kq * kq;

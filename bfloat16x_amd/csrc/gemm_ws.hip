@@ -1,0 +1,470 @@
+// Fused decode + GEMM for many rows (prefill) on gfx950: wave-specialised
+// workgroups.
+//
+// Replaces _bf16x_gemm_fused_kernel / bf16x_fused_gemm (bf16x_gemm_fused.py:31-114)
+// for M of a few hundred rows and more: y[M, N] = x[M, K] . W[N, K]^T with W
+// decoded on the fly, fp32 accumulation.  SATURATED reproduces the reference
+// kernel's numerics (code 7 -> exponent emax-7, bf16x_gemm_fused.py:84-87);
+// EXACT writes the overflow plan's entries over the decoded tile and
+// multiplies by the lossless weight.
+//
+// Measured on MI355X, and the reason for the structure:
+//  * VALU instructions in an MFMA wave's own instruction stream do not run
+//    under its MFMAs (the step time is close to the sum of both), but an
+//    MFMA wave and a VALU wave sharing a SIMD overlap.  Decoding a W element
+//    takes ~5 VALU lane-ops, so the decode runs in waves of its own.
+//  * LDS sustains ~70 B/clk per CU for writes (ds_write or direct loads) and
+//    130-220 B/clk for 16-byte reads.  Register budget (two waves per SIMD,
+//    256 registers each) limits an MFMA wave to 128 accumulators.
+//
+// A workgroup is 8 waves and owns an output tile of 256 x rows (tokens) by 128
+// W rows over a range of 64-column K steps (all of K, or one split of it when
+// the tile count alone leaves CUs idle; split partials are fp32 and summed in
+// split order by a second kernel).
+//  * Waves 4-7 decode.  Wave 4+p decodes rows 32p .. 32p+31 of the W tile at
+//    each step (lane l: row l%32, atom l/32 of the step), writes them to LDS
+//    in natural order and writes the EXACT plan entries of the same rows over
+//    them (one wave: its LDS writes land in order).  Atoms and plan entries
+//    are requested two steps ahead into registers, the plan offsets one step
+//    before their entries.
+//  * Waves 0-3 (one per SIMD) issue the MFMAs: wave c owns tokens
+//    64c .. 64c+63 and all 128 W rows, 2 x 4 accumulators of
+//    v_mfma_f32_32x32x16_bf16.  Each token row belongs to one wave, so x does
+//    not pass through LDS: a wave requests its x operands of the next step
+//    (8 16-byte loads per lane) straight into registers.  x is first
+//    rewritten in MFMA operand order (x_op_kernel, into the workspace), so
+//    each of those loads reads 1 KB contiguous: loading the operands from
+//    row-major x touches 32 rows per instruction, and the vector memory
+//    pipeline's rate in cache lines per clock, not bytes, then set the step
+//    time.  W operands come from LDS; each k-quarter first requests the next
+//    quarter's 4, then runs its 8 MFMAs.
+//  * LDS traffic is the W tile only: 16 KB written and 64 KB read per step.
+//    With the x tile staged in LDS as well (144 KB per step), the kernel ran
+//    at half this speed: LDS, not the MFMAs, set the step time.
+//  * LDS: 2 W slots of 16 KB; one barrier per step.  Tile rows are 128
+//    bytes; 16-byte chunk c of row r sits at c ^ ((r >> 1) & 7), so 16 lanes
+//    reading one logical chunk of 16 consecutive rows touch 16 different
+//    16-byte bank groups (64 banks).
+//  * MFMA k-slots: in k-quarter q, lanes 0-31 hold columns 8q .. 8q+7 of the
+//    step and lanes 32-63 columns 32+8q .. 32+8q+7, for x (A operand) and W
+//    (B operand) alike.  Result register v of lane l is
+//    D[8(v/4) + 4(l/32) + v%4][l%32]: token row, W row.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/bf16x_hip.h"
+#include "bf16x_device.h"
+#include "launch_common.h"
+
+namespace bf16x {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kStep = 64;              // K columns per step
+constexpr int kRowB = 128;             // bytes of one LDS tile row (64 bf16)
+constexpr int kBM = 256;               // tokens per tile
+constexpr int kBN = 128;               // W rows per tile
+constexpr int kWSlot = kBN * kRowB;    // 16 KB
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint64_t bytes) {
+  const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)n, 0x00020000);
+}
+
+// the words of one atom as loaded (emax as the dword holding both atoms of the step)
+struct Raw {
+  uint32_t s, m[7], d[3], ew;
+};
+
+template <bool EXACT, bool PARTIAL, bool YF32>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_ws_kernel(
+    const uint16_t* __restrict__ x, int64_t M, const uint32_t* __restrict__ sign,
+    const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
+    const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent, int64_t out_f, int64_t in_f,
+    int steps_per_split, int mtiles, int ntiles, void* __restrict__ y) {
+  __shared__ __attribute__((aligned(16))) uint8_t wlds[2 * kWSlot];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // XCD-aware tile order: blocks are dispatched round-robin over 8 XCDs; give
+  // each XCD a contiguous run of tiles, M fastest, so the M tiles that share a
+  // W tile run on one XCD at the same time and share its L2.
+  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
+  const int per = nb / 8, extra = nb - per * 8;
+  const int lb = nb >= 8 ? ((b & 7) * per + min(b & 7, extra) + (b >> 3)) : b;
+  const int64_t m0 = (int64_t)(lb % mtiles) * kBM;
+  const int nt = (lb / mtiles) % ntiles;
+  const int kb = lb / mtiles / ntiles;
+  const int64_t n0 = (int64_t)nt * kBN;
+  const int S = (int)(in_f >> 6);
+  const int s0 = kb * steps_per_split;
+  const int n = min(steps_per_split, S - s0);   // steps of this block (>= 1)
+
+  if (wave >= 4) {
+    // ===================== staging waves =====================
+    const int pw = wave - 4;                    // 0..3
+    const int64_t P = in_f >> 5;                // atoms per row
+    const int r = 32 * pw + (lane & 31), a = lane >> 5;
+    const uint64_t wat = (uint64_t)(out_f - n0) * P;   // atoms from the tile's first row
+    const __amdgpu_buffer_rsrc_t rs_ = rsrc(sign + n0 * P, wat * 4);
+    const __amdgpu_buffer_rsrc_t rm_ = rsrc(mant + n0 * P * 7, wat * 28);
+    const __amdgpu_buffer_rsrc_t rd_ = rsrc(delta + n0 * P * 3, wat * 12);
+    const __amdgpu_buffer_rsrc_t re_ = rsrc(emax2 + n0 * P, wat * 2);
+    // rows past out_f read zeros (buffer range check on the vector offset);
+    // their outputs are not stored
+    const uint32_t av = (uint32_t)(r * P) + (uint32_t)a;
+    const uint32_t vo_s = av * 4, vo_m = av * 28, vo_d = av * 12, vo_e = (uint32_t)(r * P) * 2;
+    auto load_atoms = [&](int j, Raw& t) {
+      const uint32_t s = (uint32_t)(s0 + min(j, n - 1));
+      const u32x4 m03 = __builtin_amdgcn_raw_buffer_load_b128(rm_, (int)vo_m, (int)(s * 56), 0);
+      const u32x3 m46 = __builtin_amdgcn_raw_buffer_load_b96(rm_, (int)(vo_m + 16), (int)(s * 56), 0);
+      const u32x3 d02 = __builtin_amdgcn_raw_buffer_load_b96(rd_, (int)vo_d, (int)(s * 24), 0);
+      t.s = __builtin_amdgcn_raw_buffer_load_b32(rs_, (int)vo_s, (int)(s * 8), 0);
+      // the full dword (both atoms' emax pairs) is kept raw until the decode:
+      // a value computed from a load at the load site makes the compiler wait
+      // for it there
+      t.ew = __builtin_amdgcn_raw_buffer_load_b32(re_, (int)vo_e, (int)(s * 4), 0);
+      const uint32_t c0 = m03.x, c1 = m03.y, c2 = m03.z, c3 = m03.w, c4 = m46.x, c5 = m46.y, c6 = m46.z;
+      t.m[0] = c0; t.m[1] = c1; t.m[2] = c2; t.m[3] = c3; t.m[4] = c4; t.m[5] = c5; t.m[6] = c6;
+      const uint32_t e0 = d02.x, e1 = d02.y, e2 = d02.z;
+      t.d[0] = e0; t.d[1] = e1; t.d[2] = e2;
+    };
+    const int wst = r * kRowB;                  // this lane's W row in slot 0
+    auto store_w = [&](const Raw& w, int slot) {
+      Atom t;
+      t.s = w.s;
+#pragma unroll
+      for (int i = 0; i < 7; ++i) t.m[i] = w.m[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) t.d[i] = w.d[i];
+      t.e = (uint16_t)(w.ew >> (16 * a));
+      uint32_t p[16];
+      decode_pairs(t, p);
+      uint32_t q[16];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        q[i] = perm(p[2 * i + 1], p[2 * i], 0x05040100u);      // elements 2i, 2i+1
+        q[8 + i] = perm(p[2 * i + 1], p[2 * i], 0x07060302u);  // elements 16+2i, 17+2i
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *(u32x4*)(wlds + wst + slot * kWSlot + swz(r, 4 * a + c) * 16) =
+            u32x4{q[4 * c], q[4 * c + 1], q[4 * c + 2], q[4 * c + 3]};
+    };
+
+    // EXACT plan: run of this wave's 32-row group at step s
+    const int64_t G = (out_f + 31) / 32, G2 = 2 * G;
+    const int64_t g = min(n0 / 32 + pw, G);
+    uint32_t kp_total = 0;
+    if constexpr (EXACT) kp_total = kp_off[S * G2];
+    const __amdgpu_buffer_rsrc_t rent = rsrc(kp_ent, (uint64_t)kp_total * 4);
+    const __amdgpu_buffer_rsrc_t roff = rsrc(kp_off, ((uint64_t)S * G2 + 1) * 4);
+    const uint32_t ob = (uint32_t)(2 * g) * 4, oe = (uint32_t)min(2 * g + 2, G2) * 4;
+    struct Off { uint32_t beg, end; };
+    struct Ent { uint32_t beg, end, e0, e1; };
+    auto load_off = [&](int j, Off& o) {
+      const uint32_t s = (uint32_t)(s0 + min(j, n - 1));
+      o.beg = __builtin_amdgcn_raw_buffer_load_b32(roff, (int)ob, (int)(s * G2 * 4), 0);
+      o.end = __builtin_amdgcn_raw_buffer_load_b32(roff, (int)oe, (int)(s * G2 * 4), 0);
+    };
+    auto load_ent = [&](const Off& o, Ent& e) {
+      e.beg = __builtin_amdgcn_readfirstlane(o.beg);
+      e.end = __builtin_amdgcn_readfirstlane(o.end);
+      e.e0 = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((e.beg + lane) * 4), 0, 0);
+      e.e1 = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((e.beg + lane + 64) * 4), 0, 0);
+    };
+    // The entry is used outside the branch first (the empty asm), so the
+    // compiler waits for its load there with an exact count: a loaded value
+    // first used under a divergent branch makes it wait for every
+    // outstanding load.
+    auto patch_one = [&](uint32_t e, int slot, bool live) {
+      const int rr = (int)(e >> 22) & (kBN - 1), c = (int)(e >> 16) & 63;
+      const uint32_t dst = (uint32_t)(slot * kWSlot + rr * kRowB + swz(rr, c >> 3) * 16 + (c & 7) * 2);
+      __asm__ volatile("" : "+v"(e));
+      if (live) *(uint16_t*)(wlds + dst) = (uint16_t)(e & 0xFFFFu);
+    };
+    auto patch = [&](const Ent& e, int slot) {
+      patch_one(e.e0, slot, e.beg + lane < e.end);
+      patch_one(e.e1, slot, e.beg + lane + 64 < e.end);
+      for (uint32_t k = e.beg + 128 + lane; k < e.end; k += 64)   // dense runs (rare)
+        patch_one(kp_ent[k], slot, true);
+    };
+
+    Raw A0, A1;
+    Off O0{}, O1{};
+    Ent E0{}, E1{};
+    // prologue: the requests of steps 0 and 1 (atoms, plan entries), step 0
+    // decoded, the requests of step 2.  The loads in flight at the loop entry
+    // are then the requests of 1 and 2, the pattern at the top of every
+    // iteration, so the waits the compiler derives hold on both paths into
+    // the loop
+    if constexpr (EXACT) {
+      load_off(0, O0);
+      load_off(1, O1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (EXACT) { load_ent(O0, E0); load_off(2, O0); }
+    load_atoms(0, A0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (EXACT) { load_ent(O1, E1); load_off(3, O1); }
+    load_atoms(1, A1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_w(A0, 0);
+    if constexpr (EXACT) patch(E0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (EXACT) { load_ent(O0, E0); load_off(4, O0); }
+    load_atoms(2, A0);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+
+    // iteration j: step j + 1 decoded (W slot (j + 1) & 1) from its register
+    // set, then the atoms of j + 3 requested into that set with the plan
+    // entries of j + 3 and the offsets of j + 5
+    auto iter = [&](int j, Raw& at, Off& o, Ent& e, int slot) {
+      store_w(at, slot);
+      if constexpr (EXACT) patch(e, slot);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (EXACT) { load_ent(o, e); load_off(j + 5, o); }
+      load_atoms(j + 3, at);
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    };
+    int j = 0;
+    for (; j + 1 < n; j += 2) {
+      iter(j, A1, O1, E1, 1);
+      iter(j + 1, A0, O0, E0, 0);
+    }
+    if (j < n) iter(j, A1, O1, E1, 1);
+    return;
+  }
+
+  // ===================== MFMA waves =====================
+  const int lr = lane & 31, h = lane >> 5;
+  // x operand of token tile i, k-quarter q at step s: 1 KB of x in operand
+  // order (x_op_kernel), lane l's 16 bytes at l * 16.  The block's tiles
+  // start at tile m0 / 32; rows past M hold zeros (outputs not stored).
+  const int64_t S64 = S;
+  const __amdgpu_buffer_rsrc_t rx_ = rsrc(x + m0 * in_f, (uint64_t)(((M + 31) / 32) * 32 - m0) * (uint64_t)in_f * 2);
+  const uint32_t vx0 = (uint32_t)(2 * wave * S64 * 4096 + lane * 16);
+  const uint32_t vx1 = vx0 + (uint32_t)(S64 * 4096);
+  // the x operands of one step: [token tile][k-quarter]
+  auto load_x = [&](int j, bf16x8_t (&X)[2][4]) {
+    const uint32_t ks = (uint32_t)(s0 + min(j, n - 1)) * 4096;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx_, (int)((i ? vx1 : vx0) + q * 1024), (int)ks, 0);
+        X[i][q] = __builtin_bit_cast(bf16x8_t, v);
+      }
+  };
+  // W operand of W tile jj, k-quarter q (the swizzle term depends on lr only)
+  uint32_t wo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) wo[q] = (uint32_t)(lr * kRowB + swz(lr, 4 * h + q) * 16);
+  auto load_w = [&](int q, int ws, bf16x8_t (&wb)[4]) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) wb[jj] = *(const bf16x8_t*)(wlds + wo[q] + ws * kWSlot + jj * 32 * kRowB);
+  };
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][jj][v] = 0.f;
+  auto mfma = [&](int t, const bf16x8_t (&X)[2][4], int q, const bf16x8_t (&wb)[4]) {
+    const int i = t >> 2, jj = t & 3;
+    acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[i][q], wb[jj], acc[i][jj], 0, 0, 0);
+  };
+#define BF16X_SG(mask, cnt) __builtin_amdgcn_sched_group_barrier(mask, cnt, 0)
+  bf16x8_t X0[2][4], X1[2][4], W0[4], W1[4];
+  // one step from W slot ws with x in X; x of step j + 1 requested into Xn
+  // (the set the previous step used) at the start
+  auto step = [&](int j, int ws, const bf16x8_t (&X)[2][4], bf16x8_t (&Xn)[2][4]) {
+    load_x(j + 1, Xn);
+    // quarter 0: the next quarter's W reads, then 8 MFMAs
+    load_w(1, ws, W1);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mfma(t, X, 0, W0);
+    BF16X_SG(0x020, 8);
+    BF16X_SG(0x100, 4);
+    BF16X_SG(0x008, 8);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(2, ws, W0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mfma(t, X, 1, W1);
+    BF16X_SG(0x100, 4);
+    BF16X_SG(0x008, 8);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(3, ws, W1);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mfma(t, X, 2, W0);
+    BF16X_SG(0x100, 4);
+    BF16X_SG(0x008, 8);
+    __builtin_amdgcn_sched_barrier(0);
+    // last quarter: 4 MFMAs, the barrier, the next step's quarter-0 W reads
+    // under the other 4
+#pragma unroll
+    for (int t = 0; t < 4; ++t) mfma(t, X, 3, W1);
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+    load_w(0, ws ^ 1, W0);
+#pragma unroll
+    for (int t = 4; t < 8; ++t) mfma(t, X, 3, W1);
+    BF16X_SG(0x100, 4);
+    BF16X_SG(0x008, 4);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#undef BF16X_SG
+  load_x(0, X0);
+  __syncthreads();
+  load_w(0, 0, W0);
+  int j = 0;
+  for (; j + 1 < n; j += 2) {
+    step(j, 0, X0, X1);
+    step(j + 1, 1, X1, X0);
+  }
+  if (j < n) step(j, 0, X0, X1);
+
+  // ---- store: register v of lane l -> token row 8(v/4) + 4(l/32) + v%4, W row l%32
+  float* yp = (float*)y;
+  if constexpr (PARTIAL) yp += (int64_t)kb * M * out_f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int64_t col = n0 + jj * 32 + lr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = m0 + wave * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (row < M && col < out_f) {
+          if constexpr (PARTIAL || YF32) yp[row * out_f + col] = acc[i][jj][v];
+          else ((uint16_t*)y)[row * out_f + col] = (uint16_t)f32_to_bf16_rne(acc[i][jj][v]);
+        }
+      }
+    }
+  }
+}
+
+// x [M, K] -> operand order: 32-row tile T, step s (64 columns), k-quarter q
+// is 1 KB at ((T * S + s) * 4 + q) * 1024, lane l = lr + 32 h holding row
+// 32 T + lr, columns 64 s + 32 h + 8 q .. +7 (the MFMA A operand of the
+// fused kernel).  Rows past M (up to the 32-row boundary) are zeros.  One
+// thread per 16-byte chunk, in output order.
+__global__ __launch_bounds__(256) void x_op_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t in_f,
+                                                   int64_t chunks, u32x4* __restrict__ xo) {
+  const int64_t S = in_f / 64;
+  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (int64_t)gridDim.x * 256) {
+    const int l = (int)(c & 63), q = (int)((c >> 6) & 3);
+    const int64_t ts = c >> 8, T = ts / S, s = ts - T * S;
+    const int64_t row = T * 32 + (l & 31);
+    const int64_t col = s * 64 + (l >> 5) * 32 + q * 8;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (row < M) v = *(const u32x4*)(x + row * in_f + col);
+    xo[c] = v;
+  }
+}
+
+// y = sum over splits of the fp32 partials, in split order
+template <bool YF32>
+__global__ __launch_bounds__(256) void ws_reduce_kernel(const float* __restrict__ ws, int64_t count, int nsplit,
+                                                        void* __restrict__ y) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+    float s = ws[i];
+    for (int k = 1; k < nsplit; ++k) s += ws[(int64_t)k * count + i];
+    if constexpr (YF32) ((float*)y)[i] = s;
+    else ((uint16_t*)y)[i] = (uint16_t)f32_to_bf16_rne(s);
+  }
+}
+
+struct WsShape {
+  int mtiles, ntiles, nsplit, sps;
+};
+
+// K is split while the tile count leaves CUs idle: the split minimises
+// (rounds of 256 resident blocks) x (steps per block), charging 10 % per
+// extra split (fp32 partials written and summed), smallest split on ties.
+WsShape ws_shape(int64_t M, int64_t out_f, int64_t in_f) {
+  WsShape g;
+  g.mtiles = (int)((M + kBM - 1) / kBM);
+  g.ntiles = (int)((out_f + kBN - 1) / kBN);
+  const int64_t S = in_f / kStep, tiles = (int64_t)g.mtiles * g.ntiles;
+  int best = 1;
+  double best_cost = 1e30;
+  for (int k = 1; k <= 16 && k * 4 <= S; ++k) {
+    const int64_t sps = (S + k - 1) / k, ks = (S + sps - 1) / sps;
+    const double cost = (double)((tiles * ks + 255) / 256) * sps * (1.0 + 0.10 * (ks - 1));
+    if (cost < best_cost - 1e-9) { best_cost = cost; best = (int)ks; }
+  }
+  const int64_t forced = tuning(BF16X_TUNE_GEMM_WS_SPLIT);
+  if (forced > 0) best = (int)std::min<int64_t>(forced, S);
+  g.sps = (int)((S + best - 1) / best);
+  g.nsplit = (int)((S + g.sps - 1) / g.sps);
+  return g;
+}
+
+}  // namespace
+}  // namespace bf16x
+
+using namespace bf16x;
+
+namespace {
+// workspace: x in operand order (rows rounded up to 32), then the split partials
+int64_t ws_xop_bytes(int64_t M, int64_t in_f) { return ((M + 31) / 32) * 32 * in_f * 2; }
+}  // namespace
+
+int64_t bf16x_gemm_ws_workspace(int64_t M, int64_t out_f, int64_t in_f) {
+  const WsShape g = ws_shape(M, out_f, in_f);
+  return ws_xop_bytes(M, in_f) + (g.nsplit > 1 ? (int64_t)g.nsplit * M * out_f * 4 : 0);
+}
+
+// Launch of the wave-specialised kernel; arguments checked by bf16x_gemm.
+int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m, const uint32_t* d,
+                         const uint16_t* e, const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f,
+                         int64_t in_f, bool exact, bool yf32, void* y, void* workspace, int64_t workspace_bytes,
+                         hipStream_t st) {
+  const WsShape g = ws_shape(M, out_f, in_f);
+  const bool split = g.nsplit > 1;
+  const int64_t xop = ws_xop_bytes(M, in_f);
+  if (!workspace || !aligned16(workspace) || workspace_bytes < bf16x_gemm_ws_workspace(M, out_f, in_f))
+    return BF16X_ECAPACITY;
+  if (xop >= (int64_t)0xFFFFFFFF) return BF16X_ESHAPE;
+  const int64_t grid = (int64_t)g.mtiles * g.ntiles * g.nsplit;
+  if (grid > INT32_MAX) return BF16X_ESHAPE;
+  const int64_t chunks = xop / 16;
+  hipLaunchKernelGGL(x_op_kernel, dim3((unsigned)std::min<int64_t>((chunks + 255) / 256, 8192)), dim3(256), 0, st,
+                     x, M, in_f, chunks, (u32x4*)workspace);
+  const uint16_t* xo = (const uint16_t*)workspace;
+  float* part = (float*)((uint8_t*)workspace + xop);
+  void* out = split ? (void*)part : y;
+#define BF16X_WS(EX_, PA_, YF_)                                                                                 \
+  hipLaunchKernelGGL((gemm_ws_kernel<EX_, PA_, YF_>), dim3((unsigned)grid), dim3(512), 0, st, xo, M, s, m, d, e, \
+                     kp_off, kp_ent, out_f, in_f, g.sps, g.mtiles, g.ntiles, out)
+  if (split) {
+    if (exact) BF16X_WS(true, true, false);
+    else BF16X_WS(false, true, false);
+  } else if (exact) {
+    if (yf32) BF16X_WS(true, false, true);
+    else BF16X_WS(true, false, false);
+  } else {
+    if (yf32) BF16X_WS(false, false, true);
+    else BF16X_WS(false, false, false);
+  }
+#undef BF16X_WS
+  if (split) {
+    const int64_t count = M * out_f;
+    const int64_t blocks = std::min<int64_t>((count + 255) / 256, 4096);
+    if (yf32)
+      hipLaunchKernelGGL(ws_reduce_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)part, count,
+                         g.nsplit, y);
+    else
+      hipLaunchKernelGGL(ws_reduce_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)part, count,
+                         g.nsplit, y);
+  }
+  return launch_status();
+}

@@ -731,26 +731,12 @@ using namespace bf16x;
 
 namespace {
 
-// Launch-shape overrides for tuning sweeps (BF16X_GEMV_ITERS, BF16X_GEMV_G);
-// read once per process, 0 = use the built-in heuristic.
-int env_int(const char* name) {
-  const char* s = getenv(name);
-  return s ? atoi(s) : 0;
-}
-int gemv_iters_override() {
-  static int v = env_int("BF16X_GEMV_ITERS");
-  return v;
-}
-int gemv_g_override() {
-  static int v = env_int("BF16X_GEMV_G");
-  return v;
-}
+// Launch-shape overrides (bf16x_set_tuning), 0 = use the built-in heuristic.
+int gemv_iters_override() { return (int)std::max<int64_t>(0, tuning(BF16X_TUNE_GEMV_ITERS)); }
+int gemv_g_override() { return (int)std::max<int64_t>(0, tuning(BF16X_TUNE_GEMV_G)); }
 
-// BF16X_GEMV_LONG=0 sends long rows to the split-K kernel instead.
-bool gemv_long_enabled() {
-  static bool v = getenv("BF16X_GEMV_LONG") == nullptr || env_int("BF16X_GEMV_LONG") != 0;
-  return v;
-}
+// BF16X_TUNE_GEMV_LONG = 0 sends long rows to the split-K kernel instead.
+bool gemv_long_enabled() { return tuning(BF16X_TUNE_GEMV_LONG) != 0; }
 
 // Long rows (bf16 x, 4096 < in_f <= 16384): the one-wave-per-row kernel
 // (4096 x 14336 exact: 20.5 us against 22.4 us for the split-K kernel;
@@ -877,12 +863,12 @@ int launch_gemv_g1(const void* x, const uint32_t* sign, const uint32_t* mant, co
   int iters = EPI == 1 ? 2 : (groups >= 1024 ? 2 : 1);
   if (XM != 0) {
     // every workgroup normalises x in its prologue (with its own pass over
-    // x): at least groups / 2048 row groups per workgroup (BF16X_GEMV_XM_SLOTS
-    // overrides 2048).  Measured in the Llama decode step (gate_up, 7168
+    // x): at least groups / 2048 row groups per workgroup (the override
+    // BF16X_TUNE_GEMV_XM_SLOTS replaces 2048).  Measured in the Llama decode step (gate_up, 7168
     // groups): 2048 -> 1792 workgroups, 7 per CU, 334.8 tok/s; 1024 -> 896,
     // 3.5 per CU, 327.5; 512 -> 512, 333.0; 4096 -> 3584, 309.6
     int64_t slots = 2048;
-    if (const char* e = getenv("BF16X_GEMV_XM_SLOTS")) slots = std::max<int64_t>(1, atoll(e));
+    if (const int64_t t = tuning(BF16X_TUNE_GEMV_XM_SLOTS); t > 0) slots = t;
     iters = std::max<int64_t>(iters, (groups + slots - 1) / slots);
     if (EPI == 1) iters += iters & 1;
   }

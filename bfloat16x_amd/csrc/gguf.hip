@@ -467,11 +467,8 @@ int gguf_decode_launch(const uint8_t* blocks, int64_t n_bytes, int64_t out_f, in
   return launch_status();
 }
 
-// BF16X_GGUF_LONG=0 keeps every shape on the one-pass-ahead kernel.
-bool long_enabled() {
-  static const bool v = getenv("BF16X_GGUF_LONG") == nullptr || atoi(getenv("BF16X_GGUF_LONG")) != 0;
-  return v;
-}
+// BF16X_TUNE_GGUF_LONG = 0 keeps every shape on the one-pass-ahead kernel.
+bool long_enabled() { return tuning(BF16X_TUNE_GGUF_LONG) != 0; }
 
 int gguf_gemv_launch(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes, int64_t out_f,
                      int64_t in_f, const uint32_t* ovf_off, const uint32_t* ovf_ent, void* y, int32_t y_dtype,
@@ -491,7 +488,7 @@ int gguf_gemv_launch(const void* x, int32_t x_dtype, const uint8_t* blocks, int6
     // rows per wave (as the dict GEMV): 4 from 2048 groups of 4 rows, 2 from 1024
     const int64_t groups = (out_f + 3) / 4;
     int iters = groups >= 2048 ? 4 : (groups >= 1024 ? 2 : 1);
-    if (const char* e = getenv("BF16X_GGUF_ITERS")) iters = std::max(1, std::min(atoi(e), kLongMaxIters));
+    if (const int64_t t = tuning(BF16X_TUNE_GGUF_ITERS); t > 0) iters = (int)std::min<int64_t>(t, kLongMaxIters);
     const int64_t lgrid = (groups + iters - 1) / iters;
     const size_t lds = (size_t)np * 4 * 64 * 16;
     const int xs = (np * 64 + 255) / 256;

@@ -7,7 +7,12 @@
 
 #include "../../include/bf16x_hip.h"
 
+// Kernel-choice override of bf16x_set_tuning (abi_info.cpp): -1 = automatic.
+int64_t bf16x_tuning_value(int key);
+
 namespace {
+
+inline int64_t tuning(int key) { return bf16x_tuning_value(key); }
 
 inline bool aligned2(const void* p) { return ((uintptr_t)p & 1u) == 0; }
 inline bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }

@@ -960,7 +960,7 @@ extern "C" int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, c
     return BF16X_EARG;
   const int G = (int)(n_heads / n_kv_heads);
   hipStream_t st = (hipStream_t)stream;
-  if (max_len <= kDec1MaxLen && !getenv("BF16X_ATTN_SPLIT")) {
+  if (max_len <= kDec1MaxLen && tuning(BF16X_TUNE_ATTN_SPLIT) != 1) {
 #define BF16X_DEC1(GG)                                                                                          \
   hipLaunchKernelGGL(attn_decode1_kernel<GG>, dim3((unsigned)n_kv_heads), dim3(64 * kDec1Waves), 0, st, qkv, pos, \
                      cos_sin,                                                                                   \
@@ -974,7 +974,7 @@ extern "C" int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, c
 #undef BF16X_DEC1
     return launch_status();
   }
-  if (max_len <= kDecHMaxLen && !getenv("BF16X_ATTN_SPLIT")) {
+  if (max_len <= kDecHMaxLen && tuning(BF16X_TUNE_ATTN_SPLIT) != 1) {
     hipLaunchKernelGGL((attn_decode1_kernel<1, kDecHWaves, true, kDecHBlocks>), dim3((unsigned)n_heads),
                        dim3(64 * kDecHWaves), 0, st, qkv, pos, cos_sin, (int)n_heads, (int)n_kv_heads, (int)max_len,
                        scale, k_cache, v_cache, out);

@@ -11,7 +11,6 @@ a missing library or a CPU tensor raises.
 from __future__ import annotations
 
 import collections
-import os
 
 import torch
 
@@ -325,10 +324,12 @@ def _gemm_launch(x2, s, m, d, e, out_f, in_f, plan, y, y_dtype, sub=16):
 # and runs the product as a plain library GEMM (hipBLASLt through
 # F.linear): the decode is amortised over the rows and the library GEMM runs
 # closer to the MFMA peak than the fused kernel.  Below it the fused kernel
-# avoids writing the decoded weight.  Weights with more columns than rows
-# switch at twice that many rows (measured at 4096 x 14336, M = 256: fused
-# 84 us against 94 us; at M = 512 the decode path wins, 124 against 134 us).
-GEMM_DECODE_MIN_ROWS = int(os.environ.get("BF16X_GEMM_DECODE_MIN_ROWS", "256"))
+# avoids writing and re-reading the decoded weight.  Weights with more columns
+# than rows switch at twice that many rows.  Measured (exact, rotated
+# weights): 14336x4096 M = 256: fused 72 us against 88 us, M = 384: 105
+# against 94 us; 4096x14336 M = 512: 112 against 127 us, M = 768: 172
+# against 147 us.
+GEMM_DECODE_MIN_ROWS = 320
 
 
 def _decode_min_rows(out_f: int, in_f: int) -> int:

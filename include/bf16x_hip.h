@@ -263,6 +263,37 @@ int bf16x_gguf_gemv_lossless(const void* x, int32_t x_dtype, const uint8_t* bloc
                              int64_t n_entries, void* y, int32_t y_dtype, void* workspace,
                              int64_t workspace_bytes, bf16x_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Kernel-choice overrides: a test and tuning-sweep hook with no counterpart
+ * in the reference.  Every entry point above chooses its kernel and launch
+ * shape from its arguments alone; a key set here to a value >= 0 replaces
+ * one of those choices for the whole process until it is set back to -1
+ * (automatic, the initial state).  Process-wide and unsynchronised: change
+ * it only while no other thread launches.  BF16X_EARG for an unknown key.
+ * ------------------------------------------------------------------------ */
+enum {
+  BF16X_TUNE_GEMM_SKINNY2_MAX = 0, /* largest M of the 16x16x32 few-row GEMM (0..64)              */
+  BF16X_TUNE_GEMM_SKINNY_MAX = 1,  /* largest M of the older few-row GEMM (0..128)                */
+  BF16X_TUNE_GEMM_BM = 2,          /* tile height of the tiled GEMM (32, 64, 128 or 256)          */
+  BF16X_TUNE_GEMM_SPLIT = 3,       /* K splits of the tiled GEMM                                  */
+  BF16X_TUNE_GEMM_WS_MIN_ROWS = 4, /* smallest M of the wave-specialised GEMM                     */
+  BF16X_TUNE_GEMM_WS_SPLIT = 5,    /* K splits of the wave-specialised GEMM                       */
+  BF16X_TUNE_SKINNY_WAVES = 6,     /* waves per workgroup of the older few-row GEMM (1..4)        */
+  BF16X_TUNE_SKINNY2_KQ = 7,       /* waves per row group of the 16x16x32 few-row GEMM (1, 2, 4)  */
+  BF16X_TUNE_SKINNY2_SPLIT = 8,    /* K splits of the 16x16x32 few-row GEMM                       */
+  BF16X_TUNE_GEMV_ITERS = 9,       /* row groups per workgroup of the GEMVs                       */
+  BF16X_TUNE_GEMV_G = 10,          /* K parts of the split-K GEMV (1, 2 or 4)                     */
+  BF16X_TUNE_GEMV_LONG = 11,       /* 0: rows of 4097-16384 columns on the split-K GEMV           */
+  BF16X_TUNE_GEMV_XM_SLOTS = 12,   /* workgroup target of the normalising GEMVs                   */
+  BF16X_TUNE_GGUF_LONG = 13,       /* 0: GGUF GEMV without the long-row kernel                    */
+  BF16X_TUNE_GGUF_ITERS = 14,      /* rows per wave of the GGUF long-row GEMV                     */
+  BF16X_TUNE_ATTN_SPLIT = 15,      /* 1: decode attention always on the split-key kernel          */
+  BF16X_TUNE_COUNT = 16
+};
+int bf16x_set_tuning(int32_t key, int64_t value);
+/* Current value of a key (-1 = automatic; also returned for an unknown key). */
+int64_t bf16x_get_tuning(int32_t key);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,23 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "slow: long-running CPU test")
 
 
+@pytest.fixture
+def tune():
+    """tune(key=value, ...) forces kernel choices (bf16x_set_tuning) until the
+    test ends, then restores them."""
+    import bfloat16x_amd as bx
+    active = []
+
+    def apply(**overrides):
+        t = bx.tuning(**overrides)
+        t.__enter__()
+        active.append(t)
+
+    yield apply
+    for t in reversed(active):
+        t.__exit__(None, None, None)
+
+
 @pytest.fixture(scope="session")
 def golden():
     import numpy as np

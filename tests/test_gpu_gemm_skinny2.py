@@ -8,7 +8,6 @@ bf16 give y = the fp32 accumulation of one pass) and held to 1e-3 of the
 float64 product: a dropped or misplaced term (about 1/sqrt(in_f) of an
 output) fails it.  Rows of I pick W columns bit for bit, which pins the
 MFMA operand and result layouts and every overflow patch."""
-import os
 
 import numpy as np
 import pytest
@@ -66,11 +65,11 @@ def test_skinny2_fp32_product(bx, M, out_f, in_f):
 
 @pytest.mark.parametrize("kq", ["1", "2"])
 @pytest.mark.parametrize("M,out_f,in_f", [(5, 130, 4096), (33, 72, 1024), (48, 384, 14336), (64, 200, 2048)])
-def test_skinny2_waves_per_row_group(bx, monkeypatch, kq, M, out_f, in_f):
-    """The other wave-per-row-group counts (BF16X_SKINNY2_KQ=1: one wave walks
-    every step of its rows; 2: two waves take alternate steps) give the same
-    fp32 product: the default is 4 up to 32 rows and 2 above."""
-    monkeypatch.setenv("BF16X_SKINNY2_KQ", kq)
+def test_skinny2_waves_per_row_group(bx, tune, kq, M, out_f, in_f):
+    """The other wave-per-row-group counts (override skinny2_kq = 1: one wave
+    walks every step of its rows; 2: two waves take alternate steps) give the
+    same fp32 product: the default is 4 up to 32 rows and 2 above."""
+    tune(skinny2_kq=int(kq))
     bits, d, g, plan = _weight(bx, out_f, in_f, seed=M + out_f + 7)
     x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M + 1)).to(torch.bfloat16).float()
     dn = _np(d)
@@ -100,17 +99,16 @@ def test_skinny2_identity_is_bit_exact(bx, M):
             assert np.array_equal(got, ref[:, start:start + cols]), (start, p is None)
 
 
-def test_skinny2_matches_previous_kernel(bx, monkeypatch):
-    """Same inputs through the 32x32-MFMA few-row kernel (selected by
-    BF16X_GEMM_SKINNY2_MAX=0): both accumulate in fp32, so the bf16 outputs
-    agree to within one rounding of either."""
+def test_skinny2_matches_previous_kernel(bx):
+    """Same inputs through the 32x32-MFMA few-row kernel (selected by the
+    override gemm_skinny2_max = 0): both accumulate in fp32, so the bf16
+    outputs agree to within one rounding of either."""
     out_f, in_f, M = 320, 4096, 24
     bits, d, g, plan = _weight(bx, out_f, in_f, seed=4)
     x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(DEV)
     y2 = _gemm(bx, x, g, out_f, in_f, plan).float().cpu().numpy()
-    monkeypatch.setenv("BF16X_GEMM_SKINNY2_MAX", "0")
-    y1 = _gemm(bx, x, g, out_f, in_f, plan).float().cpu().numpy()
-    monkeypatch.delenv("BF16X_GEMM_SKINNY2_MAX")
+    with bx.tuning(gemm_skinny2_max=0):
+        y1 = _gemm(bx, x, g, out_f, in_f, plan).float().cpu().numpy()
     ref = dc.gemm_ref(_np(d), x.float().cpu().numpy(), saturated=False)
     check_tol(y2, ref)
     check_tol(y1, ref)
@@ -158,4 +156,4 @@ def test_skinny2_full_size(bx, M, out_f, in_f):
     y = _gemm(bx, x, g, out_f, in_f, plan)
     mx, med = check_tol(y.float().cpu().numpy(), y_ref)
     print("skinny2 full-size rel err max %.2e median %.2e" % (mx, med), flush=True)
-    assert os.environ.get("BF16X_GEMM_SKINNY2_MAX") is None
+    assert bx._lib.lib().bf16x_get_tuning(bx._lib.TUNE_KEYS["gemm_skinny2_max"]) == -1

@@ -160,15 +160,15 @@ def test_attention(bx, T, pos, L):
                                         (16, 2, 100, 640), (8, 1, 31, 48), (32, 8, 3000, 4096),
                                         (64, 8, 511, 1024), (32, 8, 1, 640), (32, 8, 199, 200),
                                         (32, 8, 767, 768), (64, 8, 700, 768), (8, 2, 400, 769), (32, 8, 257, 260)])
-def test_attention_decode_matches_two_launch_path(bx, H, KV, pos, L, split, monkeypatch):
+def test_attention_decode_matches_two_launch_path(bx, H, KV, pos, L, split, tune):
     """The fused one-token kernel against rope_kv + attention on the same
     inputs: the same cache rows and outputs (one bf16 rounding apart at
     most), and the fp32 reference.  Contexts up to 256 keys run the
     one-workgroup-per-KV-head kernel, up to 768 the one-workgroup-per-query-
-    head kernel, unless BF16X_ATTN_SPLIT selects the split kernel (which
-    longer contexts always use)."""
+    head kernel, unless the override attn_split = 1 selects the split kernel
+    (which longer contexts always use)."""
     if split:
-        monkeypatch.setenv("BF16X_ATTN_SPLIT", "1")
+        tune(attn_split=1)
     assert llama.attention_decode_supported(H, KV, L)
     qkv = rnd((H + 2 * KV) * 128, 13)
     kc0, vc0 = rnd((KV, L, 128), 14), rnd((KV, L, 128), 15)
