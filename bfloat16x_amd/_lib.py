@@ -52,6 +52,7 @@ PROTOTYPES = {
     "bf16x_gguf_decode": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i64, _P, _c_i32, _P]),
     "bf16x_gguf_gemv_workspace": (_c_i64, [_c_i64]),
     "bf16x_gguf_gemv": (ctypes.c_int, [_P, _c_i32, _P, _c_i64, _c_i64, _c_i64, _P, _c_i32, _P, _c_i64, _P]),
+    "bf16x_gguf_gemv_noalloc": (ctypes.c_int, [_P, _c_i32, _P, _c_i64, _c_i64, _c_i64, _P, _c_i32, _P]),
     "bf16x_gguf_ovf_pack_host": (ctypes.c_int, [_P, _c_i64, _c_i64, _P, _P, _c_i64, ctypes.POINTER(_c_i64), _c_i32]),
     "bf16x_gguf_ovf_check_host": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i64, _P, _P, _c_i64]),
     "bf16x_gguf_decode_lossless": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i64, _P, _P, _c_i64, _P, _c_i32, _P]),

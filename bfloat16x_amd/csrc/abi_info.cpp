@@ -12,7 +12,8 @@ extern "C" const char* bf16x_status_string(int status) {
     case BF16X_ESHAPE: return "unsupported or inconsistent shape";
     case BF16X_ESTREAM_LEN: return "a packed stream is shorter than the shape requires";
     case BF16X_ETABLE: return "malformed overflow table";
-    case BF16X_ECAPACITY: return "output capacity too small";
+    case BF16X_ECAPACITY:
+      return "capacity too small (an output or workspace, or the fixed scratch of an allocation-free entry point)";
     case BF16X_ESUB: return "sub != 16 is not supported by the GPU kernels";
     case BF16X_EDTYPE: return "unsupported dtype code";
     default: return status > 0 ? "HIP runtime error" : "unknown status";

@@ -8,6 +8,8 @@
 // packed dict's atom in AoS order, so the atom decoder of bf16x_device.h
 // serves both formats (decode_pairs<true>).
 #include <hip/hip_runtime.h>
+
+#include <mutex>
 #include <stdint.h>
 #include <stdlib.h>
 
@@ -545,6 +547,58 @@ extern "C" int bf16x_gguf_decode_lossless(const uint8_t* blocks, int64_t n_bytes
 }
 
 extern "C" int64_t bf16x_gguf_gemv_workspace(int64_t in_f) { return in_f > 0 ? in_f * 2 : 0; }
+
+// ---------------------------------------------------------------------------
+// Allocation-free GEMV (bf16x_gguf_gemv_noalloc): the workspace of
+// bf16x_gguf_gemv (x rearranged in decode order, in_f * 2 bytes) lives in a
+// fixed device array instead, so callers that cannot allocate (graph
+// capture, serving loops) pass only inputs and outputs.  Each GPU the library
+// runs on holds its own copy of the array for the life of the process; every
+// call on that GPU reuses it, so calls that overlap on one GPU race.  The
+// array is written in full before it is read, so it needs no clearing.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int64_t kNoAllocScratchBytes = (int64_t)1 << 17;   // in_f <= 65536
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];   // this GPU's address of `scratch`, looked up once
+
+// Device address of the current GPU's copy of `scratch`.  The host-side name
+// of a __device__ array is only a stand-in; the address is looked up with
+// the device current and kept per device.
+int scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return BF16X_EARG;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return BF16X_OK;
+}
+}  // namespace
+
+extern "C" int bf16x_gguf_gemv_noalloc(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes,
+                                       int64_t out_f, int64_t in_f, void* y, int32_t y_dtype,
+                                       bf16x_stream_t stream) {
+  if (!x || !y || !blocks) return BF16X_EARG;
+  if (in_f * 2 > kNoAllocScratchBytes) return BF16X_ECAPACITY;
+  void* ws = nullptr;
+  const int rc = scratch_ptr(&ws);
+  if (rc) return rc;
+  return gguf_gemv_launch(x, x_dtype, blocks, n_bytes, out_f, in_f, nullptr, nullptr, y, y_dtype, ws,
+                          kNoAllocScratchBytes, (hipStream_t)stream);
+}
 
 extern "C" int bf16x_gguf_gemv(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes, int64_t out_f,
                                int64_t in_f, void* y, int32_t y_dtype, void* workspace, int64_t workspace_bytes,

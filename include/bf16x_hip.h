@@ -228,6 +228,17 @@ int bf16x_gguf_gemv(const void* x, int32_t x_dtype, const uint8_t* blocks, int64
                     int64_t out_f, int64_t in_f, void* y, int32_t y_dtype,
                     void* workspace, int64_t workspace_bytes, bf16x_stream_t stream);
 
+/* bf16x_gguf_gemv without a workspace argument.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under
+ * graph capture, tight serving loops, harnesses that forbid it).  The
+ * workspace is a fixed 128 KB device array inside the library, one copy per
+ * GPU held for the life of the process, so in_f is limited to 65536
+ * (BF16X_ECAPACITY beyond it).  The stream must belong to the current
+ * device.  Every call on a GPU uses that GPU's array: calls that overlap on
+ * one GPU race.  Allocates nothing. */
+int bf16x_gguf_gemv_noalloc(const void* x, int32_t x_dtype, const uint8_t* blocks, int64_t n_bytes,
+                            int64_t out_f, int64_t in_f, void* y, int32_t y_dtype, bf16x_stream_t stream);
+
 /* GGUF lossless side table (bf16x_gguf_block.py:96-193).  The table of a
  * weight [rows, cols] is the reference's blob without its 8-byte header:
  *   row_off uint32 [rows + 1]   entry index where each row starts
