@@ -1017,7 +1017,9 @@ extern "C" int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t f
 extern "C" int bf16x_greedy(const uint16_t* logits, int64_t vocab, int64_t* token, int32_t* state, int32_t* history,
                             int64_t history_len, bf16x_stream_t stream) {
   if (!logits || !token || !state || (!history && history_len > 0) || history_len < 0) return BF16X_EARG;
-  if (vocab <= 0 || vocab > INT32_MAX - 8 * 1024 || history_len > INT32_MAX) return BF16X_ESHAPE;
+  // greedy_kernel steps its int indices by 1024 * 8 per batch element and
+  // 16 elements per batch: the last batch's indices must not overflow
+  if (vocab <= 0 || vocab > INT32_MAX - 2 * 1024 * 8 * 16 || history_len > INT32_MAX) return BF16X_ESHAPE;
   if (!aligned16(logits) || !aligned4(state) || ((uintptr_t)token & 7u)) return BF16X_EARG;
   hipLaunchKernelGGL(greedy_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, (int)vocab, token, state,
                      history, (int)history_len);

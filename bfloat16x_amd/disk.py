@@ -29,6 +29,7 @@ built: it raises.
 """
 from __future__ import annotations
 
+import dataclasses
 import gc
 import json
 import os
@@ -43,75 +44,114 @@ from .codec import Bf16xPlan, bf16x_quantize, build_plan_host, stream_words
 KIND = "bf16x-v1"
 _DEFAULT_SKIP = ("embed", "lm_head")
 _STREAM_BITS = (("sign", 1), ("mant", 7), ("delta", 3))
+_STREAM_FIELDS = (("sign", "sign_packed"), ("mant", "mant_packed"), ("delta", "delta_packed"))
 
-__all__ = ["KIND", "pack_model_to_disk", "pack_linear", "load_meta", "Bf16xStreamLinear",
+__all__ = ["KIND", "LinearRecord", "pack_model_to_disk", "pack_linear", "load_meta", "Bf16xStreamLinear",
            "replace_linears_from_packed"]
 
 
-def _pad1(t: torch.Tensor) -> torch.Tensor:
-    return torch.cat([t, torch.zeros(1, dtype=t.dtype)])
+@dataclasses.dataclass
+class LinearRecord:
+    """One packed linear as it goes to disk: the bf16x-v1 arrays in file
+    order, the meta fields and the optional bias (bf16)."""
+    name: str
+    arrays: dict
+    out_f: int
+    in_f: int
+    n_fix: int
+    bias: torch.Tensor | None = None
+
+    def meta(self, keys: dict) -> dict:
+        m = dict(keys)
+        m.update(out_f=self.out_f, in_f=self.in_f, N=self.out_f * self.in_f, n_fix=self.n_fix)
+        return m
+
+
+def _with_zero_word(words: torch.Tensor) -> torch.Tensor:
+    """A stream with the format's trailing zero word."""
+    out = torch.zeros(words.numel() + 1, dtype=words.dtype)
+    out[:-1] = words
+    return out
 
 
 def pack_linear(w: torch.Tensor, sub: int = 16) -> dict:
     """One weight [out_f, in_f] -> the six on-disk arrays of bf16x-v1
     (CPU tensors) and its meta fields."""
     p = bf16x_quantize(w.detach().to(torch.bfloat16).cpu(), sub=sub)
-    oi = p["delta_ovf_idx"].to(torch.int64)
-    ov = p["delta_ovf_val"].to(torch.int64)
-    keep = ov > 7
-    oi, ov = oi[keep], ov[keep]
-    arrays = {"sign": _pad1(p["sign_packed"]), "mant": _pad1(p["mant_packed"]),
-              "delta": _pad1(p["delta_packed"]), "emax": p["emax"],
-              "ovf_i": oi.contiguous(), "ovf_v": ov.to(torch.int32).contiguous()}
+    needed = p["delta_ovf_val"] > 7             # delta == 7 decodes exactly from the 3-bit code
+    arrays = {key: _with_zero_word(p[field]) for key, field in _STREAM_FIELDS}
+    arrays["emax"] = p["emax"]
+    arrays["ovf_i"] = p["delta_ovf_idx"][needed].to(torch.int64).contiguous()
+    arrays["ovf_v"] = p["delta_ovf_val"][needed].to(torch.int32).contiguous()
     out_f, in_f = int(p["out_f"]), int(p["in_f"])
-    return {"arrays": arrays, "out_f": out_f, "in_f": in_f, "N": out_f * in_f, "n_fix": int(oi.numel())}
+    return {"arrays": arrays, "out_f": out_f, "in_f": in_f, "N": out_f * in_f, "n_fix": int(needed.sum())}
+
+
+def _record(name: str, linear: nn.Linear, sub: int) -> LinearRecord:
+    pk = pack_linear(linear.weight.data, sub=sub)
+    bias = linear.bias.data.detach().to(torch.bfloat16).cpu().contiguous() if linear.bias is not None else None
+    return LinearRecord(name, pk["arrays"], pk["out_f"], pk["in_f"], pk["n_fix"], bias)
+
+
+def _packable(model: nn.Module, min_numel: int, skip) -> list:
+    """(name, module) of the linears to pack, in module order."""
+    return [(name, mod) for name, mod in model.named_modules()
+            if isinstance(mod, nn.Linear) and mod.weight.numel() >= min_numel
+            and not any(s in name for s in skip)]
+
+
+class _BlobWriter:
+    """Collects records into one safetensors dict and the meta table; the key
+    of array k of linear n is "n.k"."""
+
+    def __init__(self):
+        self.tensors: dict = {}
+        self.table: dict = {}
+        self.nbytes = 0
+
+    def _put(self, key: str, t: torch.Tensor) -> str:
+        self.tensors[key] = t
+        self.nbytes += t.numel() * t.element_size()
+        return key
+
+    def add(self, rec: LinearRecord):
+        keys = {k: self._put(f"{rec.name}.{k}", t) for k, t in rec.arrays.items()}
+        if rec.bias is not None:
+            keys["bias"] = self._put(f"{rec.name}.bias", rec.bias)
+        self.table[rec.name] = rec.meta(keys)
+
+    def write(self, out_prefix: str) -> tuple:
+        from safetensors.torch import save_file
+        path = out_prefix + ".safetensors"
+        save_file(self.tensors, path, metadata={"format": "bf16x"})
+        with open(out_prefix + ".meta.json", "w") as f:
+            json.dump({"kind": KIND, "tensors": self.table}, f)
+        return path, os.path.getsize(path)
 
 
 @torch.no_grad()
 def pack_model_to_disk(model, out_prefix, min_numel=4096, sub=16, skip=_DEFAULT_SKIP, verbose=True):
     """Pack every nn.Linear (numel >= min_numel, name containing none of
     `skip`) into <out_prefix>.safetensors + <out_prefix>.meta.json; each
-    original weight (and bias) is dropped once packed (pack_to_disk.py:40-105).
-    Returns (n_packed, packed_bytes)."""
-    from safetensors.torch import save_file
-
-    blobs = {}
-    meta = {"kind": KIND, "tensors": {}}
-    total, n = 0, 0
-    t0 = time.time()
-    for name, mod in list(model.named_modules()):
-        if not isinstance(mod, nn.Linear):
-            continue
-        if mod.weight.numel() < min_numel or any(s in name for s in skip):
-            continue
-        pk = pack_linear(mod.weight.data, sub=sub)
-        m = {}
-        for key, val in pk["arrays"].items():
-            gk = f"{name}.{key}"
-            blobs[gk] = val
-            total += val.numel() * val.element_size()
-            m[key] = gk
-        m["out_f"], m["in_f"], m["N"], m["n_fix"] = pk["out_f"], pk["in_f"], pk["N"], pk["n_fix"]
-        if mod.bias is not None:
-            gk = f"{name}.bias"
-            blobs[gk] = mod.bias.data.detach().to(torch.bfloat16).cpu().contiguous()
-            total += blobs[gk].numel() * blobs[gk].element_size()
-            m["bias"] = gk
-            mod.bias.data = torch.empty(0)
-        meta["tensors"][name] = m
-        mod.weight.data = torch.empty(0)
-        del pk
-        n += 1
-        if verbose and n % 50 == 0:
-            print(f"  {n} packed, blob {total / 1e9:.1f}GB, {time.time() - t0:.0f}s", flush=True)
-    pack_path, meta_path = out_prefix + ".safetensors", out_prefix + ".meta.json"
-    save_file(blobs, pack_path, metadata={"format": "bf16x"})
-    with open(meta_path, "w") as f:
-        json.dump(meta, f)
+    original weight (and bias) is released as soon as it is packed, so the
+    host holds at most one unpacked layer beside the packed ones
+    (pack_to_disk.py:40-105).  Returns (n_packed, packed_bytes)."""
+    writer = _BlobWriter()
+    start = time.time()
+    chosen = _packable(model, min_numel, skip)
+    for i, (name, lin) in enumerate(chosen, 1):
+        writer.add(_record(name, lin, sub))
+        lin.weight.data = torch.empty(0)
+        if lin.bias is not None:
+            lin.bias.data = torch.empty(0)
+        if verbose and i % 50 == 0:
+            print(f"[bf16x-v1] packed {i}/{len(chosen)} linears ({writer.nbytes / 1e9:.2f} GB) "
+                  f"after {time.time() - start:.0f} s", flush=True)
+    path, size = writer.write(out_prefix)
     if verbose:
-        print(f"  -> {pack_path} ({os.path.getsize(pack_path) / 1e9:.2f}GB, {n} linears)", flush=True)
+        print(f"[bf16x-v1] wrote {path}: {len(chosen)} linears, {size / 1e9:.2f} GB", flush=True)
     gc.collect()
-    return n, total
+    return len(chosen), writer.nbytes
 
 
 def load_meta(out_prefix) -> dict:
@@ -157,39 +197,41 @@ class Bf16xStreamLinear(nn.Module):
     mode "fused" (default): fused decode+GEMV for one token, the exact
     decode+GEMM dispatch otherwise; mode "decode": exact decode into a
     buffer shared per device, then F.linear (the reference module's two
-    steps).  Both use the lossless weight."""
+    steps).  Both use the lossless weight.  Built from one meta entry and its
+    arrays (checked first), with the streams moved to `device` once."""
 
-    def __init__(self):
+    def __init__(self, entry: dict, blob: dict, device=None, name: str = "?"):
         super().__init__()
-        raise RuntimeError("use from_packed()")
+        _check_entry(name, entry, blob)
+        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self.out_features, self.in_features = int(entry["out_f"]), int(entry["in_f"])
+        self.N = self.out_features * self.in_features
+        self.n_fix = int(entry.get("n_fix", 0))
+        self.resident = True
+        self.mode = "fused"
+        self.gpu = {k: blob[k].contiguous().to(dev) for k in ("sign", "mant", "delta", "emax")}
+        self.plan: Bf16xPlan = build_plan_host(self._host_dict(blob), device=dev)
+        b = blob.get("bias")
+        self.bias = b.to(dev, torch.bfloat16) if b is not None else None
+
+    def _host_dict(self, blob: dict) -> dict:
+        """The packed dict the plan builder reads: the file's table (entries
+        with true delta > 7) in the dict's dtypes."""
+        table = (blob["ovf_i"].to(torch.int32), blob["ovf_v"].to(torch.uint8)) if self.n_fix else \
+            (torch.zeros(0, dtype=torch.int32), torch.zeros(0, dtype=torch.uint8))
+        d = {field: blob[key] for key, field in _STREAM_FIELDS}
+        d.update(emax=blob["emax"], delta_ovf_idx=table[0], delta_ovf_val=table[1], out_f=self.out_features,
+                 in_f=self.in_features, sub=16)
+        return d
 
     @classmethod
     def from_packed(cls, entry: dict, blob: dict, resident: bool = True, device=None, name: str = "?"):
+        """The reference's constructor (pack_to_disk.py:108-140): only the
+        resident variant exists here."""
         if not resident:
             raise NotImplementedError("the non-resident (pinned host, per-call copy) variant is not built: "
                                       "keep the streams resident on the GPU")
-        _check_entry(name, entry, blob)
-        obj = cls.__new__(cls)
-        nn.Module.__init__(obj)
-        dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-        obj.out_features, obj.in_features = int(entry["out_f"]), int(entry["in_f"])
-        obj.N = int(entry["N"])
-        obj.n_fix = int(entry.get("n_fix", 0))
-        obj.resident = True
-        obj.mode = "fused"
-        obj.gpu = {k: blob[k].contiguous().to(dev) for k in ("sign", "mant", "delta", "emax")}
-        host = {"sign_packed": blob["sign"], "mant_packed": blob["mant"], "delta_packed": blob["delta"],
-                "emax": blob["emax"], "out_f": obj.out_features, "in_f": obj.in_features, "sub": 16}
-        if obj.n_fix:
-            host["delta_ovf_idx"] = blob["ovf_i"].to(torch.int32)
-            host["delta_ovf_val"] = blob["ovf_v"].to(torch.uint8)
-        else:
-            host["delta_ovf_idx"] = torch.zeros(0, dtype=torch.int32)
-            host["delta_ovf_val"] = torch.zeros(0, dtype=torch.uint8)
-        obj.plan: Bf16xPlan = build_plan_host(host, device=dev)
-        b = blob.get("bias")
-        obj.bias = b.to(dev, torch.bfloat16) if b is not None else None
-        return obj
+        return cls(entry, blob, device=device, name=name)
 
     def decoded_weight(self) -> torch.Tensor:
         g = self.gpu
@@ -215,6 +257,15 @@ class Bf16xStreamLinear(nn.Module):
         return y if b is None else y + b.to(y.dtype)
 
 
+_ARRAY_KEYS = ("sign", "mant", "delta", "emax", "ovf_i", "ovf_v", "bias")
+
+
+def _install(model: nn.Module, name: str, module: nn.Module):
+    """Put `module` at the dotted path `name` of `model`."""
+    parent_name, _, leaf = name.rpartition(".")
+    setattr(model.get_submodule(parent_name) if parent_name else model, leaf, module)
+
+
 @torch.no_grad()
 def replace_linears_from_packed(model, out_prefix, resident_fn=None, keep_rest_bf16=True, verbose=True,
                                 device=None):
@@ -225,31 +276,26 @@ def replace_linears_from_packed(model, out_prefix, resident_fn=None, keep_rest_b
     is moved to the GPU.  Returns the number replaced."""
     from safetensors import safe_open
 
-    meta = load_meta(out_prefix)
-    n = 0
-    t0 = time.time()
+    table = load_meta(out_prefix)
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    start = time.time()
+    linears = [(name, mod) for name, mod in model.named_modules() if isinstance(mod, nn.Linear)]
+    replaced = 0
     with safe_open(out_prefix + ".safetensors", framework="pt", device="cpu") as sf:
-        for name, mod in list(model.named_modules()):
-            if not isinstance(mod, nn.Linear):
+        for name, lin in linears:
+            entry = table.get(name)
+            if entry is None:
+                if keep_rest_bf16:
+                    lin.weight.data = lin.weight.data.to(torch.bfloat16)
                 continue
-            if name in meta:
-                entry = meta[name]
-                blob = {k: sf.get_tensor(entry[k]) for k in ("sign", "mant", "delta", "emax", "ovf_i", "ovf_v",
-                                                              "bias") if entry.get(k)}
-                res = resident_fn(name) if resident_fn else True
-                new = Bf16xStreamLinear.from_packed(entry, blob, resident=res, device=dev, name=name)
-                parent = model
-                parts = name.split(".")
-                for q in parts[:-1]:
-                    parent = getattr(parent, q)
-                setattr(parent, parts[-1], new)
-                mod.weight.data = torch.empty(0)
-                n += 1
-                del blob
-            elif keep_rest_bf16:
-                mod.weight.data = mod.weight.data.to(torch.bfloat16)
+            arrays = {k: sf.get_tensor(entry[k]) for k in _ARRAY_KEYS if entry.get(k)}
+            resident = resident_fn(name) if resident_fn is not None else True
+            _install(model, name, Bf16xStreamLinear.from_packed(entry, arrays, resident=resident, device=dev,
+                                                                name=name))
+            lin.weight.data = torch.empty(0)
+            replaced += 1
     model.to(dev)
     if verbose:
-        print(f"[bf16x] {n} linears from disk in {time.time() - t0:.1f}s (resident)", flush=True)
-    return n
+        print(f"[bf16x-v1] loaded {replaced} linears from {out_prefix}.safetensors in "
+              f"{time.time() - start:.1f} s, streams resident on {dev}", flush=True)
+    return replaced

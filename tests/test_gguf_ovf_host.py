@@ -146,3 +146,18 @@ def test_host_check_accepts_good_and_rejects_tampered():
 
     for f in (swap, offcol, flip_sign, bad_off, col_range):
         assert _check(packed, blob, t=f) == _lib.ETABLE, f.__name__
+
+
+@pytest.mark.parametrize("case,exact", [("selftest", False), ("dense", True), ("empty", False)])
+def test_pack_ovf_bytes_match_reference(golden, case, exact):
+    """The serialized side table, byte for byte, against blobs the reference's
+    pack_ovf wrote (tests/golden/make_golden.py): header, row offsets and the
+    {u16 col, u16 bits} entries in row-then-column order, from the oracle and
+    from the C++ packer behind gguf.pack_ovf."""
+    x = golden[f"gguf_ovf_{case}_x"]
+    want = golden[f"gguf_ovf_{case}_blob"].tobytes()
+    bits = go.fp32_to_bf16_bits(x) if not exact else (x.view(np.uint32) >> 16).astype(np.uint16)
+    assert go.pack_ovf_bits(bits) == want
+    assert gguf.pack_ovf(x, bf16_exact=exact) == want
+    if case == "dense":
+        assert int(np.frombuffer(want[4:8], dtype=np.uint32)[0]) > x.shape[0] * 8   # many entries per row

@@ -381,7 +381,7 @@ def test_norm_in_gemv_decode_matches_prefill(small):
 
 @torch.no_grad()
 @pytest.mark.parametrize("out_f,in_f,dense", [(512, 1024, False), (1000, 6144, False), (384, 14336, False),
-                                              (4100, 6144, True)])
+                                              (4100, 6144, True), (8192, 4096, False), (8200, 6144, True)])
 def test_residual_and_prenormed_gemv(bx, out_f, in_f, dense):
     """bf16x_gemv_residual: y bit-identical to bf16x_gemv, residual_out =
     bf16(y + residual_in) bit for bit, the slots add up to sum(h^2).
