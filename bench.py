@@ -194,9 +194,11 @@ def bench_sweep(bx, dev, stream) -> dict:
 
 
 def bench_gguf(bx, dev, stream) -> list:
-    """GGUF decode+GEMV (batch 1) and decode+GEMM (M = 512) at 8192x28672 and
-    28672x8192, two rotating copies (> 2x the Infinity Cache); max abs
-    reconstruction error of the decode against bf16(w)."""
+    """GGUF decode+GEMV (batch 1) and decode+GEMM (M = 512, the fused kernel;
+    decode into a temporary + F.linear and F.linear on the bf16 weight timed
+    beside it) at 8192x28672 and 28672x8192, two rotating copies (> 2x the
+    Infinity Cache); max abs reconstruction error of the decode against
+    bf16(w)."""
     import numpy as np
     out = []
     for out_f, in_f in ((8192, 28672), (28672, 8192)):
@@ -223,6 +225,10 @@ def bench_gguf(bx, dev, stream) -> list:
         del dec_out
         xm = torch.randn(512, in_f, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
         sec_m = time_launches(lambda i: bx.gguf.gguf_gemm(xm, copies[i % 2], out_f, in_f), 10, 2, stream)
+        sec_ml = time_launches(lambda i: bx.gguf.gguf_gemm(xm, copies[i % 2], out_f, in_f, ovf=ovf), 10, 2, stream)
+        sec_md = time_launches(lambda i: torch.nn.functional.linear(xm, bx.gguf.gguf_decode(copies[i % 2], out_f,
+                                                                                              in_f)), 10, 2, stream)
+        sec_mb = time_launches(lambda i: torch.nn.functional.linear(xm, wb), 10, 2, stream)
         sec_lv = time_launches(lambda i: bx.gguf.gguf_gemv(x, copies[i % 2], out_f, in_f, ovf=ovf), 200, 20, stream)
         dec_l = bx.gguf.gguf_decode(copies[0], out_f, in_f, ovf=ovf)
         lossless_exact = bool(torch.equal(dec_l.view(torch.int16), wb.view(torch.int16)))
@@ -241,16 +247,50 @@ def bench_gguf(bx, dev, stream) -> list:
                "decode_us": round(sec_d * 1e6, 2),
                "gemm_M512_us": round(sec_m * 1e6, 2),
                "gemm_M512_tflops": round(2.0 * 512 * out_f * in_f / sec_m / 1e12, 1),
+               "gemm_M512_mfma_frac": round(2.0 * 512 * out_f * in_f / sec_m / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+               "gemm_M512_decode_then_linear_us": round(sec_md * 1e6, 2),
+               "bf16_linear_M512_us": round(sec_mb * 1e6, 2),
                "clamped_fraction": round(clamped, 5), "max_abs_reconstruction_error": err,
                "lossless": {"table_bytes": len(blob), "entries": ovf.n_entries,
                             "bpw": round((nbytes + len(blob)) * 8 / (out_f * in_f), 3),
                             "decode_bit_exact": lossless_exact,
                             "gemv_us": round(sec_lv * 1e6, 2),
                             "gemv_GBps": round((vbytes + len(blob)) / sec_lv / 1e9, 1),
-                            "decode_us": round(sec_ld * 1e6, 2)}}
+                            "decode_us": round(sec_ld * 1e6, 2),
+                            "gemm_M512_us": round(sec_ml * 1e6, 2)}}
         log(f"gguf {ent}")
         out.append(ent)
     return out
+
+
+def bench_gemm_case(bx, dev, stream, case: str, reps: int) -> dict:
+    """One fused decode+GEMM case run `reps` times back to back (the
+    workload of the kernel-trace and counter profiles of the GEMM kernels):
+    dict = the packed dict of the configuration weights with its plan
+    (exact), gguf = GGUF blocks of Student-t (df 3) x 0.015 weights."""
+    import numpy as np
+    fmt, shape, rows = case.split(":")
+    out_f, in_f = (int(v) for v in shape.split("x"))
+    M = int(rows)
+    xm = torch.randn(M, in_f, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(dev)
+    if fmt == "dict":
+        d = bx.bf16x_quantize(bench_weight(out_f, in_f, seed=0).to(dev))
+        plan = bx.build_plan_host(d, device=dev)
+        plan.kplan()
+        fn = lambda i: bx.bf16x_gemm(xm, d["sign_packed"], d["mant_packed"], d["delta_packed"], d["emax"], out_f,
+                                     in_f, plan=plan, path="fused")
+    elif fmt == "gguf":
+        rng = np.random.default_rng(0)
+        w = (rng.standard_t(3, size=(out_f, in_f)) * 0.015).astype(np.float32)
+        b = bx.gguf.device_blocks(bx.gguf.quantize_blocks(w), dev)
+        del w
+        fn = lambda i: bx.gguf.gguf_gemm_fused(xm, b, out_f, in_f)
+    else:
+        raise ValueError(f"unknown case format {fmt!r}")
+    sec = time_launches(fn, reps, 2, stream)
+    flops = 2.0 * M * out_f * in_f
+    return {"case": case, "reps": reps, "us": round(sec * 1e6, 2), "tflops": round(flops / sec / 1e12, 1),
+            "mfma_frac": round(flops / sec / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
 def bench_llama(bx, dev, prompt_len: int = 512, n_new: int = 128, reps: int = 2) -> dict:
@@ -358,9 +398,11 @@ def main():
                     help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 2048],
                     help="activation rows of the decode+GEMM lines (configuration 3)")
-    ap.add_argument("--only", choices=("llama", "gguf", "sweep"),
+    ap.add_argument("--only", choices=("llama", "gguf", "sweep", "gemm"),
                     help="run one secondary workload alone and print its record (a measurement / profiling mode, "
-                         "not the benchmark line)")
+                         "not the benchmark line); gemm: one fused decode+GEMM case (--case) --steps times")
+    ap.add_argument("--case", default="dict:14336x4096:512",
+                    help="--only gemm case, FORMAT:OUTxIN:M with FORMAT dict (exact, packed dict) or gguf")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -372,7 +414,9 @@ def main():
         torch.cuda.set_device(dev)
         st_ = torch.cuda.current_stream(dev)
         rec = (bench_llama(bx, dev) if args.only == "llama" else
-               bench_gguf(bx, dev, st_) if args.only == "gguf" else bench_sweep(bx, dev, st_))
+               bench_gguf(bx, dev, st_) if args.only == "gguf" else
+               bench_gemm_case(bx, dev, st_, args.case, args.steps) if args.only == "gemm" else
+               bench_sweep(bx, dev, st_))
         print(json.dumps({"only": args.only, "record": rec}), flush=True)
         return
 

@@ -58,6 +58,10 @@ PROTOTYPES = {
     "bf16x_gguf_decode_lossless": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i64, _P, _P, _c_i64, _P, _c_i32, _P]),
     "bf16x_gguf_gemv_lossless": (ctypes.c_int, [_P, _c_i32, _P, _c_i64, _c_i64, _c_i64, _P, _P, _c_i64, _P, _c_i32,
                                                 _P, _c_i64, _P]),
+    "bf16x_gguf_gemm_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64]),
+    "bf16x_gguf_gemm": (ctypes.c_int, [_P, _c_i32, _c_i64, _P, _c_i64, _P, _P, _c_i64, _c_i64, _P, _c_i32, _P,
+                                       _c_i64, _P]),
+    "bf16x_gguf_kplan_build": (ctypes.c_int, [_P, _P, _c_i64, _c_i64, _P, _P, _P]),
     # include/bf16x_llama.h
     "bf16x_rmsnorm": (ctypes.c_int, [_P, _P, _c_i64, _P, _P, _P, _c_i64, _c_i64, ctypes.c_float, _c_i32, _P]),
     "bf16x_rope_kv": (ctypes.c_int, [_P, _c_i64, _P, _P, _c_i64, _c_i64, _c_i64, _c_i64, _P, _P, _P, _P]),

@@ -373,8 +373,10 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
 // g*32 + r, which are sorted by column; lanes 0-15 and 16-31 make the runs of
 // the 16-row groups 2g and 2g + 1.  Pass 1 counts each (step, 16-row group)
 // run, a one-block scan turns counts into offsets, pass 2 writes the entries.
+// GE: entries of the GGUF side table (column | bits << 16) instead of the row
+// plan's (column << 16 | bits).
 // ---------------------------------------------------------------------------
-template <bool FILL>
+template <bool FILL, bool GE>
 __global__ __launch_bounds__(64) void kplan_pass_kernel(const uint32_t* __restrict__ tile_off,
                                                         const uint32_t* __restrict__ tile_ent, int64_t out_f,
                                                         int S, int G2, uint32_t* __restrict__ kp_off,
@@ -386,7 +388,8 @@ __global__ __launch_bounds__(64) void kplan_pass_kernel(const uint32_t* __restri
   uint32_t p = live ? tile_off[row] : 0, pe = live ? tile_off[row + 1] : 0;
   for (int s = 0; s < S; ++s) {
     uint32_t c = 0;
-    while (p + c < pe && (tile_ent[p + c] >> 22) == (uint32_t)s) ++c;   // column >> 6 == s
+    // column >> 6 == s
+    while (p + c < pe && ((GE ? tile_ent[p + c] & 0xFFFFu : tile_ent[p + c] >> 16) >> 6) == (uint32_t)s) ++c;
     uint32_t incl = c;                   // inclusive prefix over the lanes
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
@@ -404,7 +407,8 @@ __global__ __launch_bounds__(64) void kplan_pass_kernel(const uint32_t* __restri
       const uint32_t base = kp_off[(int64_t)s * G2 + h] + (lane >= 16 ? incl - lo : incl) - c;
       for (uint32_t i = 0; i < c; ++i) {
         const uint32_t e = tile_ent[p + i];
-        kp_ent[base + i] = ((uint32_t)(row & 255) << 22) | (((e >> 16) & 63u) << 16) | (e & 0xFFFFu);
+        const uint32_t col = GE ? e & 0xFFFFu : e >> 16, bits = GE ? e >> 16 : e & 0xFFFFu;
+        kp_ent[base + i] = ((uint32_t)(row & 255) << 22) | ((col & 63u) << 16) | bits;
       }
     }
     p += c;
@@ -445,27 +449,40 @@ extern "C" int64_t bf16x_kplan_size(int64_t out_f, int64_t in_f) {
   return (in_f / kBK) * 2 * ((out_f + kGroupRows - 1) / kGroupRows) + 1;
 }
 
-extern "C" int bf16x_kplan_build(const uint32_t* tile_off, const uint32_t* tile_ent, int64_t out_f, int64_t in_f,
-                                 uint32_t* kp_off, uint32_t* kp_ent, bf16x_stream_t stream) {
+namespace {
+template <bool GE>
+int kplan_build(const uint32_t* tile_off, const uint32_t* tile_ent, int64_t out_f, int64_t in_f, uint32_t* kp_off,
+                uint32_t* kp_ent, bf16x_stream_t stream) {
   if (!tile_off || !tile_ent || !kp_off || !kp_ent) return BF16X_EARG;
   if (out_f <= 0 || in_f <= 0 || (in_f % kBK) != 0 || tiles_per_row(in_f) != 1) return BF16X_ESHAPE;
   const int64_t S = in_f / kBK, G = (out_f + kGroupRows - 1) / kGroupRows, G2 = 2 * G;
   if (G2 > INT32_MAX || S * G2 + 1 > (int64_t)INT32_MAX) return BF16X_ESHAPE;
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(kplan_pass_kernel<false>, dim3((unsigned)G), dim3(64), 0, st, tile_off, tile_ent, out_f, (int)S,
-                     (int)G2, kp_off, kp_ent);
+  hipLaunchKernelGGL((kplan_pass_kernel<false, GE>), dim3((unsigned)G), dim3(64), 0, st, tile_off, tile_ent, out_f,
+                     (int)S, (int)G2, kp_off, kp_ent);
   hipLaunchKernelGGL(kplan_scan_kernel, dim3(1), dim3(1024), 0, st, kp_off, S * G2);
-  hipLaunchKernelGGL(kplan_pass_kernel<true>, dim3((unsigned)G), dim3(64), 0, st, tile_off, tile_ent, out_f, (int)S,
-                     (int)G2, kp_off, kp_ent);
+  hipLaunchKernelGGL((kplan_pass_kernel<true, GE>), dim3((unsigned)G), dim3(64), 0, st, tile_off, tile_ent, out_f,
+                     (int)S, (int)G2, kp_off, kp_ent);
   return launch_status();
+}
+}  // namespace
+
+extern "C" int bf16x_kplan_build(const uint32_t* tile_off, const uint32_t* tile_ent, int64_t out_f, int64_t in_f,
+                                 uint32_t* kp_off, uint32_t* kp_ent, bf16x_stream_t stream) {
+  return kplan_build<false>(tile_off, tile_ent, out_f, in_f, kp_off, kp_ent, stream);
+}
+
+extern "C" int bf16x_gguf_kplan_build(const uint32_t* row_off, const uint32_t* entries, int64_t out_f, int64_t in_f,
+                                      uint32_t* kp_off, uint32_t* kp_ent, bf16x_stream_t stream) {
+  return kplan_build<true>(row_off, entries, out_f, in_f, kp_off, kp_ent, stream);
 }
 
 // wave-specialised kernel (gemm_ws.hip): M >= ws_rows()
 int64_t bf16x_gemm_ws_workspace(int64_t M, int64_t out_f, int64_t in_f);
 int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m, const uint32_t* d,
-                         const uint16_t* e, const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f,
-                         int64_t in_f, bool exact, bool yf32, void* y, void* workspace, int64_t workspace_bytes,
-                         hipStream_t st);
+                         const uint16_t* e, const uint8_t* blocks, const uint32_t* kp_off, const uint32_t* kp_ent,
+                         int64_t out_f, int64_t in_f, bool exact, bool yf32, void* y, void* workspace,
+                         int64_t workspace_bytes, hipStream_t st);
 
 // few-row kernel (gemm_skinny.hip): M <= skinny_rows()
 int bf16x_gemm_skinny_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m, const uint32_t* d,
@@ -583,7 +600,7 @@ extern "C" int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M, const int32
   }
   if (use_ws(M, in_f)) {
     rc = bf16x_gemm_ws_launch((const uint16_t*)x, M, (const uint32_t*)sign, (const uint32_t*)mant,
-                              (const uint32_t*)delta, (const uint16_t*)emax, kp_off, kp_ent, out_f, in_f,
+                              (const uint32_t*)delta, (const uint16_t*)emax, nullptr, kp_off, kp_ent, out_f, in_f,
                               mode == BF16X_EXACT, y_dtype == BF16X_F32, y, workspace, workspace_bytes, st);
     return rc ? rc : launch_status();
   }

@@ -52,6 +52,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "../../include/bf16x_hip.h"
 #include "bf16x_device.h"
 #include "launch_common.h"
@@ -79,13 +81,20 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint64_t b
 struct Raw {
   uint32_t s, m[7], d[3], ew;
 };
+// a GGUF block as loaded: the 48 bytes from the dword at or below it
+struct RawG {
+  u32x4 q0, q1, q2;
+};
 
-template <bool EXACT, bool PARTIAL, bool YF32>
+// GG: W is GGUF half-blocks (`blocks`, 46 bytes per 32 elements, row-major;
+// the dict stream pointers are unused), decoded with the zero marker
+// (bf16x_gguf_block.py:76-87).  Otherwise W is the packed dict.
+template <bool GG, bool EXACT, bool PARTIAL, bool YF32>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_ws_kernel(
     const uint16_t* __restrict__ x, int64_t M, const uint32_t* __restrict__ sign,
     const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
-    const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent, int64_t out_f, int64_t in_f,
-    int steps_per_split, int mtiles, int ntiles, void* __restrict__ y) {
+    const uint8_t* __restrict__ blocks, const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent,
+    int64_t out_f, int64_t in_f, int steps_per_split, int mtiles, int ntiles, void* __restrict__ y) {
   __shared__ __attribute__((aligned(16))) uint8_t wlds[2 * kWSlot];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -109,41 +118,65 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const int pw = wave - 4;                    // 0..3
     const int64_t P = in_f >> 5;                // atoms per row
     const int r = 32 * pw + (lane & 31), a = lane >> 5;
+    using RawT = typename std::conditional<GG, RawG, Raw>::type;
     const uint64_t wat = (uint64_t)(out_f - n0) * P;   // atoms from the tile's first row
-    const __amdgpu_buffer_rsrc_t rs_ = rsrc(sign + n0 * P, wat * 4);
-    const __amdgpu_buffer_rsrc_t rm_ = rsrc(mant + n0 * P * 7, wat * 28);
-    const __amdgpu_buffer_rsrc_t rd_ = rsrc(delta + n0 * P * 3, wat * 12);
-    const __amdgpu_buffer_rsrc_t re_ = rsrc(emax2 + n0 * P, wat * 2);
+    __amdgpu_buffer_rsrc_t rs_, rm_, rd_, re_, rb_;
+    uint32_t vo_s = 0, vo_m = 0, vo_d = 0, vo_e = 0, vo_b = 0, sh = 0;
     // rows past out_f read zeros (buffer range check on the vector offset);
     // their outputs are not stored
     const uint32_t av = (uint32_t)(r * P) + (uint32_t)a;
-    const uint32_t vo_s = av * 4, vo_m = av * 28, vo_d = av * 12, vo_e = (uint32_t)(r * P) * 2;
-    auto load_atoms = [&](int j, Raw& t) {
+    if constexpr (GG) {
+      // the tile's first block starts at a multiple of 4 bytes (n0 % 128 == 0);
+      // the range is the rest of the blocks rounded up to 4 bytes, which the
+      // caller guarantees readable.  Block (r, 2s + a) is at av * 46 + s * 92:
+      // its offset modulo 4 (0 or 2) does not depend on s.
+      rb_ = rsrc(blocks + (uint64_t)n0 * P * 46, (wat * 46 + 3) & ~3ull);
+      vo_b = av * 46;
+      sh = (vo_b & 2u) * 8u;
+      vo_b &= ~3u;
+    } else {
+      rs_ = rsrc(sign + n0 * P, wat * 4);
+      rm_ = rsrc(mant + n0 * P * 7, wat * 28);
+      rd_ = rsrc(delta + n0 * P * 3, wat * 12);
+      re_ = rsrc(emax2 + n0 * P, wat * 2);
+      vo_s = av * 4; vo_m = av * 28; vo_d = av * 12; vo_e = (uint32_t)(r * P) * 2;
+    }
+    auto load_atoms = [&](int j, RawT& t) {
       const uint32_t s = (uint32_t)(s0 + min(j, n - 1));
-      const u32x4 m03 = __builtin_amdgcn_raw_buffer_load_b128(rm_, (int)vo_m, (int)(s * 56), 0);
-      const u32x3 m46 = __builtin_amdgcn_raw_buffer_load_b96(rm_, (int)(vo_m + 16), (int)(s * 56), 0);
-      const u32x3 d02 = __builtin_amdgcn_raw_buffer_load_b96(rd_, (int)vo_d, (int)(s * 24), 0);
-      t.s = __builtin_amdgcn_raw_buffer_load_b32(rs_, (int)vo_s, (int)(s * 8), 0);
-      // the full dword (both atoms' emax pairs) is kept raw until the decode:
-      // a value computed from a load at the load site makes the compiler wait
-      // for it there
-      t.ew = __builtin_amdgcn_raw_buffer_load_b32(re_, (int)vo_e, (int)(s * 4), 0);
-      const uint32_t c0 = m03.x, c1 = m03.y, c2 = m03.z, c3 = m03.w, c4 = m46.x, c5 = m46.y, c6 = m46.z;
-      t.m[0] = c0; t.m[1] = c1; t.m[2] = c2; t.m[3] = c3; t.m[4] = c4; t.m[5] = c5; t.m[6] = c6;
-      const uint32_t e0 = d02.x, e1 = d02.y, e2 = d02.z;
-      t.d[0] = e0; t.d[1] = e1; t.d[2] = e2;
+      if constexpr (GG) {
+        t.q0 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)vo_b, (int)(s * 92), 0);
+        t.q1 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)(vo_b + 16), (int)(s * 92), 0);
+        t.q2 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)(vo_b + 32), (int)(s * 92), 0);
+      } else {
+        const u32x4 m03 = __builtin_amdgcn_raw_buffer_load_b128(rm_, (int)vo_m, (int)(s * 56), 0);
+        const u32x3 m46 = __builtin_amdgcn_raw_buffer_load_b96(rm_, (int)(vo_m + 16), (int)(s * 56), 0);
+        const u32x3 d02 = __builtin_amdgcn_raw_buffer_load_b96(rd_, (int)vo_d, (int)(s * 24), 0);
+        t.s = __builtin_amdgcn_raw_buffer_load_b32(rs_, (int)vo_s, (int)(s * 8), 0);
+        // the full dword (both atoms' emax pairs) is kept raw until the decode:
+        // a value computed from a load at the load site makes the compiler wait
+        // for it there
+        t.ew = __builtin_amdgcn_raw_buffer_load_b32(re_, (int)vo_e, (int)(s * 4), 0);
+        const uint32_t c0 = m03.x, c1 = m03.y, c2 = m03.z, c3 = m03.w, c4 = m46.x, c5 = m46.y, c6 = m46.z;
+        t.m[0] = c0; t.m[1] = c1; t.m[2] = c2; t.m[3] = c3; t.m[4] = c4; t.m[5] = c5; t.m[6] = c6;
+        const uint32_t e0 = d02.x, e1 = d02.y, e2 = d02.z;
+        t.d[0] = e0; t.d[1] = e1; t.d[2] = e2;
+      }
     };
     const int wst = r * kRowB;                  // this lane's W row in slot 0
-    auto store_w = [&](const Raw& w, int slot) {
-      Atom t;
-      t.s = w.s;
-#pragma unroll
-      for (int i = 0; i < 7; ++i) t.m[i] = w.m[i];
-#pragma unroll
-      for (int i = 0; i < 3; ++i) t.d[i] = w.d[i];
-      t.e = (uint16_t)(w.ew >> (16 * a));
+    auto store_w = [&](const RawT& w, int slot) {
       uint32_t p[16];
-      decode_pairs(t, p);
+      if constexpr (GG) {
+        decode_pairs<true>(gguf_atom(GgufRaw{w.q0, w.q1, w.q2, sh}), p);
+      } else {
+        Atom t;
+        t.s = w.s;
+#pragma unroll
+        for (int i = 0; i < 7; ++i) t.m[i] = w.m[i];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) t.d[i] = w.d[i];
+        t.e = (uint16_t)(w.ew >> (16 * a));
+        decode_pairs(t, p);
+      }
       uint32_t q[16];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -194,7 +227,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         patch_one(kp_ent[k], slot, true);
     };
 
-    Raw A0, A1;
+    RawT A0, A1;
     Off O0{}, O1{};
     Ent E0{}, E1{};
     // prologue: the requests of steps 0 and 1 (atoms, plan entries), step 0
@@ -224,7 +257,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // iteration j: step j + 1 decoded (W slot (j + 1) & 1) from its register
     // set, then the atoms of j + 3 requested into that set with the plan
     // entries of j + 3 and the offsets of j + 5
-    auto iter = [&](int j, Raw& at, Off& o, Ent& e, int slot) {
+    auto iter = [&](int j, RawT& at, Off& o, Ent& e, int slot) {
       store_w(at, slot);
       if constexpr (EXACT) patch(e, slot);
       __builtin_amdgcn_sched_barrier(0);
@@ -423,11 +456,13 @@ int64_t bf16x_gemm_ws_workspace(int64_t M, int64_t out_f, int64_t in_f) {
   return ws_xop_bytes(M, in_f) + (g.nsplit > 1 ? (int64_t)g.nsplit * M * out_f * 4 : 0);
 }
 
-// Launch of the wave-specialised kernel; arguments checked by bf16x_gemm.
+// Launch of the wave-specialised kernel; arguments checked by the caller
+// (bf16x_gemm for the packed dict; bf16x_gguf_gemm for GGUF blocks, given
+// as `blocks` with the dict pointers null).
 int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m, const uint32_t* d,
-                         const uint16_t* e, const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f,
-                         int64_t in_f, bool exact, bool yf32, void* y, void* workspace, int64_t workspace_bytes,
-                         hipStream_t st) {
+                         const uint16_t* e, const uint8_t* blocks, const uint32_t* kp_off, const uint32_t* kp_ent,
+                         int64_t out_f, int64_t in_f, bool exact, bool yf32, void* y, void* workspace,
+                         int64_t workspace_bytes, hipStream_t st) {
   const WsShape g = ws_shape(M, out_f, in_f);
   const bool split = g.nsplit > 1;
   const int64_t xop = ws_xop_bytes(M, in_f);
@@ -442,29 +477,35 @@ int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const 
   const uint16_t* xo = (const uint16_t*)workspace;
   float* part = (float*)((uint8_t*)workspace + xop);
   void* out = split ? (void*)part : y;
-#define BF16X_WS(EX_, PA_, YF_)                                                                                 \
-  hipLaunchKernelGGL((gemm_ws_kernel<EX_, PA_, YF_>), dim3((unsigned)grid), dim3(512), 0, st, xo, M, s, m, d, e, \
-                     kp_off, kp_ent, out_f, in_f, g.sps, g.mtiles, g.ntiles, out)
-  if (split) {
-    if (exact) BF16X_WS(true, true, false);
-    else BF16X_WS(false, true, false);
-  } else if (exact) {
-    if (yf32) BF16X_WS(true, false, true);
-    else BF16X_WS(true, false, false);
-  } else {
-    if (yf32) BF16X_WS(false, false, true);
-    else BF16X_WS(false, false, false);
-  }
+#define BF16X_WS1(GG_, EX_, PA_, YF_)                                                                            \
+  hipLaunchKernelGGL((gemm_ws_kernel<GG_, EX_, PA_, YF_>), dim3((unsigned)grid), dim3(512), 0, st, xo, M, s, m, d, \
+                     e, blocks, kp_off, kp_ent, out_f, in_f, g.sps, g.mtiles, g.ntiles, out)
+#define BF16X_WS(GG_)                                        \
+  do {                                                       \
+    if (split) {                                             \
+      if (exact) BF16X_WS1(GG_, true, true, false);          \
+      else BF16X_WS1(GG_, false, true, false);               \
+    } else if (exact) {                                      \
+      if (yf32) BF16X_WS1(GG_, true, false, true);           \
+      else BF16X_WS1(GG_, true, false, false);               \
+    } else {                                                 \
+      if (yf32) BF16X_WS1(GG_, false, false, true);          \
+      else BF16X_WS1(GG_, false, false, false);              \
+    }                                                        \
+  } while (0)
+  if (blocks) BF16X_WS(true);
+  else BF16X_WS(false);
 #undef BF16X_WS
+#undef BF16X_WS1
   if (split) {
     const int64_t count = M * out_f;
-    const int64_t blocks = std::min<int64_t>((count + 255) / 256, 4096);
+    const int64_t blocks_r = std::min<int64_t>((count + 255) / 256, 4096);
     if (yf32)
-      hipLaunchKernelGGL(ws_reduce_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)part, count,
-                         g.nsplit, y);
+      hipLaunchKernelGGL(ws_reduce_kernel<true>, dim3((unsigned)blocks_r), dim3(256), 0, st, (const float*)part,
+                         count, g.nsplit, y);
     else
-      hipLaunchKernelGGL(ws_reduce_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)part, count,
-                         g.nsplit, y);
+      hipLaunchKernelGGL(ws_reduce_kernel<false>, dim3((unsigned)blocks_r), dim3(256), 0, st, (const float*)part,
+                         count, g.nsplit, y);
   }
   return launch_status();
 }

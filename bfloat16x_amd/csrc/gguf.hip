@@ -616,3 +616,39 @@ extern "C" int bf16x_gguf_gemv_lossless(const void* x, int32_t x_dtype, const ui
   return gguf_gemv_launch(x, x_dtype, blocks, n_bytes, out_f, in_f, row_off, entries, y, y_dtype, workspace,
                           workspace_bytes, (hipStream_t)stream);
 }
+
+// ---------------------------------------------------------------------------
+// Fused decode + GEMM over GGUF blocks: the wave-specialised kernel of
+// gemm_ws.hip with its block loader (46-byte blocks, zero-marker decode).
+// The lossless table enters as the step-major plan of bf16x_gguf_kplan_build.
+// ---------------------------------------------------------------------------
+int64_t bf16x_gemm_ws_workspace(int64_t M, int64_t out_f, int64_t in_f);
+int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const uint32_t* m, const uint32_t* d,
+                         const uint16_t* e, const uint8_t* blocks, const uint32_t* kp_off, const uint32_t* kp_ent,
+                         int64_t out_f, int64_t in_f, bool exact, bool yf32, void* y, void* workspace,
+                         int64_t workspace_bytes, hipStream_t st);
+
+extern "C" int64_t bf16x_gguf_gemm_workspace(int64_t M, int64_t out_f, int64_t in_f) {
+  if (M <= 0 || out_f <= 0 || in_f < 64 || (in_f % 64) != 0) return 0;
+  return bf16x_gemm_ws_workspace(M, out_f, in_f);
+}
+
+extern "C" int bf16x_gguf_gemm(const void* x, int32_t x_dtype, int64_t M, const uint8_t* blocks, int64_t n_bytes,
+                               const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f, int64_t in_f, void* y,
+                               int32_t y_dtype, void* workspace, int64_t workspace_bytes, bf16x_stream_t stream) {
+  int rc = check_gguf(blocks, n_bytes, out_f, in_f);
+  if (rc) return rc;
+  if (!x || !y || (kp_off == nullptr) != (kp_ent == nullptr)) return BF16X_EARG;
+  if (x_dtype != BF16X_BF16 || (y_dtype != BF16X_BF16 && y_dtype != BF16X_F32)) return BF16X_EDTYPE;
+  if (M <= 0 || (in_f % 64) != 0) return BF16X_ESHAPE;
+  if (kp_off && in_f > 65536) return BF16X_ESHAPE;   // the plan's 16-bit columns
+  // 32-bit buffer offsets: x in operand order, and one 128-row tile of blocks
+  if (M * in_f * 2 >= (int64_t)0xFFFFFFFF || 128 * (in_f / 32) * kBlockBytes >= (int64_t)0xFFFFFFF0)
+    return BF16X_ESHAPE;
+  if (!aligned16(x) || !aligned4(blocks) || !aligned4(y)) return BF16X_EARG;
+  if (kp_off && (!aligned4(kp_off) || !aligned4(kp_ent))) return BF16X_EARG;
+  rc = bf16x_gemm_ws_launch((const uint16_t*)x, M, nullptr, nullptr, nullptr, nullptr, blocks, kp_off, kp_ent, out_f,
+                            in_f, kp_off != nullptr, y_dtype == BF16X_F32, y, workspace, workspace_bytes,
+                            (hipStream_t)stream);
+  return rc ? rc : launch_status();
+}

@@ -274,6 +274,29 @@ int bf16x_gguf_gemv_lossless(const void* x, int32_t x_dtype, const uint8_t* bloc
                              int64_t n_entries, void* y, int32_t y_dtype, void* workspace,
                              int64_t workspace_bytes, bf16x_stream_t stream);
 
+/* Fused decode + GEMM over GGUF blocks: y[M, out_f] = x[M, in_f] . W^T with
+ * W decoded on the fly (dequantize_blocks, bf16x_gguf_block.py:76-87),
+ * fp32 accumulation (bf16 MFMA).  No counterpart in the reference, which
+ * stops at the decode; it replaces dequantize_blocks followed by a matmul.
+ * kp_off / kp_ent: NULL for the near-lossless weight, or the step-major plan
+ * of the lossless table (bf16x_gguf_kplan_build) for the exact weight.
+ * x: dev bf16 [M, in_f], 16-byte aligned; y: dev [M, out_f] of y_dtype
+ * (BF16X_BF16 or BF16X_F32).  Requires in_f % 64 == 0 (and in_f <= 65536
+ * with a plan).  Workspace: bf16x_gguf_gemm_workspace(M, out_f, in_f) bytes,
+ * 16-byte aligned (x in operand order, fp32 partials when K is split);
+ * smaller returns BF16X_ECAPACITY.  Device. */
+int64_t bf16x_gguf_gemm_workspace(int64_t M, int64_t out_f, int64_t in_f);
+int bf16x_gguf_gemm(const void* x, int32_t x_dtype, int64_t M, const uint8_t* blocks, int64_t n_bytes,
+                    const uint32_t* kp_off, const uint32_t* kp_ent, int64_t out_f, int64_t in_f, void* y,
+                    int32_t y_dtype, void* workspace, int64_t workspace_bytes, bf16x_stream_t stream);
+
+/* Step-major plan of a lossless GGUF table for bf16x_gguf_gemm: the table's
+ * (row_off, entries) in place of bf16x_kplan_build's row plan, same output
+ * (kp_off [bf16x_kplan_size(out_f, in_f)], kp_ent [n_entries, >= 1 word]).
+ * Requires in_f % 64 == 0 and in_f <= 65536.  Device. */
+int bf16x_gguf_kplan_build(const uint32_t* row_off, const uint32_t* entries, int64_t out_f, int64_t in_f,
+                           uint32_t* kp_off, uint32_t* kp_ent, bf16x_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Kernel-choice overrides: a test and tuning-sweep hook with no counterpart
  * in the reference.  Every entry point above chooses its kernel and launch

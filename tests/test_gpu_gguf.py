@@ -75,6 +75,43 @@ def test_gemv_and_gemm(bx, shape):
     check_tol(ym.float().cpu().numpy(), xm.double().numpy() @ wdec.T)
 
 
+# fused decode + GEMM: ragged M (rows past M in a 256-row tile), ragged out_f
+# (rows past out_f in a 128-row tile), split K (few tiles) and whole K
+@pytest.mark.parametrize("shape", [(256, 4096), (1000, 1024), (200, 4224), (96, 28672)])
+def test_gemm_fused(bx, shape):
+    out_f, in_f = shape
+    print("gguf gemm fused", shape, flush=True)
+    w = gc.student_t_weights(out_f, in_f, seed=5)
+    blocks = bx.gguf.quantize_blocks(w)
+    wdec = gc.dequantize_blocks(blocks).astype(np.float64).reshape(out_f, in_f)
+    b = bx.gguf.device_blocks(blocks, DEV)
+    for M in (1, 37, 256, 300):
+        xm = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+        ref = xm.double().numpy() @ wdec.T
+        for dt in (torch.bfloat16, torch.float32):
+            y = bx.gguf.gguf_gemm_fused(xm.to(DEV), b, out_f, in_f, out_dtype=dt)
+            assert y.dtype == dt and y.shape == (M, out_f)
+            check_tol(y.float().cpu().numpy(), ref)
+    # the dispatching entry, leading dims kept: one row (GEMV), the fused
+    # GEMM's range, above it (decode + library GEMM)
+    for lead in ((1, 1), (3, 1), (2, 150), (1, bx.gguf.GGUF_GEMM_MAX_ROWS + 1)):
+        x3 = torch.randn(*lead, in_f, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
+        y3 = bx.gguf.gguf_gemm(x3.to(DEV), b, out_f, in_f)
+        assert y3.shape == (*lead, out_f) and y3.dtype == torch.bfloat16
+        check_tol(y3.float().cpu().numpy().reshape(-1, out_f), x3.double().numpy().reshape(-1, in_f) @ wdec.T)
+
+
+def test_gemm_fused_refuses(bx):
+    from bfloat16x_amd import Bf16xError
+    w = gc.student_t_weights(8, 96, seed=1)
+    b = bx.gguf.device_blocks(bx.gguf.quantize_blocks(w), DEV)
+    x = torch.zeros(4, 96, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(Bf16xError):
+        bx.gguf.gguf_gemm_fused(x, b, 8, 96)          # in_f % 64 != 0
+    with pytest.raises(ValueError):
+        bx.gguf.gguf_gemm_fused(x.float(), b, 8, 96)  # x not bf16
+
+
 @pytest.mark.parametrize("shape", [(8192, 28672), (28672, 8192)])
 def test_config5_full_size(bx, shape):
     """Configuration 5 shapes: encode (C++) -> decode (GPU) keeps sign and
@@ -101,3 +138,15 @@ def test_config5_full_size(bx, shape):
     y = bx.gguf.gguf_gemv(x, b, out_f, in_f)
     y_ref = (dec.float() @ x.float()).double().cpu().numpy()
     check_tol(y.float().cpu().numpy(), y_ref)
+    # decode + GEMM at M = 512 (the configuration's prefill shape), fused,
+    # against an fp64 product of the decoded weight.  Outputs near zero are
+    # measured against a floor of 1e-3 rms: there the fp32 accumulation over
+    # K = 28672 (1792 sequential MFMA adds, ~2.5e-6 rms each output) is the
+    # error, up to ~0.5e-2 of the floor; bf16 outputs add their rounding.
+    xm = torch.randn(512, in_f, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).to(DEV)
+    ym_ref = (xm.double() @ dec.double().t()).cpu().numpy()
+    y32 = bx.gguf.gguf_gemm_fused(xm, b, out_f, in_f, out_dtype=torch.float32)
+    print("M=512 fp32 out: rel err max %.3e median %.3e" % check_tol(y32.cpu().numpy(), ym_ref), flush=True)
+    ym = bx.gguf.gguf_gemm(xm, b, out_f, in_f)
+    print("M=512 bf16 out: rel err max %.3e median %.3e" % check_tol(ym.float().cpu().numpy(), ym_ref,
+                                                                       max_tol=1.5e-2), flush=True)

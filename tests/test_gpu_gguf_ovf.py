@@ -79,6 +79,13 @@ def test_lossless_gemv_gemm(g, kind, shape):
         check_tol(y.float().cpu().numpy(), ref)
     xm = torch.randn(7, shape[1], generator=torch.Generator().manual_seed(7)).to(torch.bfloat16)
     check_tol(g.gguf_gemm(xm.to(DEV), blocks, *shape, ovf=t).float().cpu().numpy(), xm.double().numpy() @ wb.T)
+    if shape[1] % 64 == 0:
+        # the fused GEMM with the table's step-major plan (two row counts:
+        # one partial tile, and more than one 256-row tile)
+        for M in (7, 300):
+            xm = torch.randn(M, shape[1], generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+            y = g.gguf_gemm_fused(xm.to(DEV), blocks, *shape, out_dtype=torch.float32, ovf=t)
+            check_tol(y.cpu().numpy(), xm.double().numpy() @ wb.T)
 
 
 def test_tampered_table_refused(g):
