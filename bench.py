@@ -85,24 +85,81 @@ def time_launches(fn, n_launch: int, warmup: int, stream, queued: bool = False) 
     return t0.elapsed_time(t1) / 1e3 / n_launch
 
 
+def gemm_kernel_name(M: int, out_f: int, in_f: int) -> str:
+    """The kernel the fused GEMM path runs for M rows (bf16x_gemm's default
+    dispatch in the C ABI)."""
+    if M <= 64 and in_f % 128 == 0:
+        return "gemm_skinny2_kernel (16x16x32 MFMA, few rows)"
+    if M <= 32:
+        return "gemm_skinny_kernel"
+    if M >= 192:
+        return "gemm_ws_kernel (wave-specialised, 32x32x16 MFMA)"
+    return "gemm_kernel (tiled)"
+
+
+def gemm_roofline(ent: dict, flops: float, out_f: int, in_f: int) -> None:
+    """MFMA roofline entries of one decode+GEMM line: the fused kernel's and
+    the default dispatch's achieved TFLOP/s against the dense bf16 peak."""
+    from bfloat16x_amd import ops
+    M = ent["M"]
+    for path in ("fused", "auto"):
+        tf = flops / (ent[f"{path}_us"] * 1e-6) / 1e12
+        ent[f"roofline_{path}"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)}
+    ent["fused_kernel"] = gemm_kernel_name(M, out_f, in_f)
+    ent["auto_path"] = "decode + F.linear (hipBLASLt)" if M >= ops._decode_min_rows(out_f, in_f) else "fused"
+
+
 def cpu_baseline(d: dict, alg_bytes_full: int, rows: int, reps: int) -> dict:
-    """The reference's CPU decode+matmul path (restated in oracle/cpu_path.py)
-    on the first `rows` rows, median of `reps` timed passes after one warm-up
-    (13-20 s of CPU work at the defaults), scaled to compressed GB/s."""
+    """The reference's CPU path (restated in oracle/cpu_path.py: BF16XLinear,
+    opqk_linear.py:360-377 decode, :390-404 forward) on the host cores, in
+    the same run as the GPU lines.  `value`: decode+matmul (batch 1) on the
+    first `rows` rows of the configuration-2 weight, median of `reps` timed
+    passes after one warm-up, scaled to compressed GB/s.  Beside it, each
+    timed the same way: decode only (same rows); the configuration-1 decode
+    (2048x1536, whole weight); decode+matmul with M = 16 and M = 256
+    activation rows (configuration 3) on a sample of the rows, in TFLOP/s."""
     from oracle.cpu_path import CpuBf16xLinear
+    import bfloat16x_amd as bx
     torch.set_num_threads(os.cpu_count() or 1)
+
+    def timed(fn, n):
+        fn()  # warm-up
+        ts = []
+        for _ in range(n):
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        ts.sort()
+        return ts[len(ts) // 2], sum(ts)
+
     lin = CpuBf16xLinear(d, tile=1024)
     x = torch.randn(1, d["in_f"], generator=torch.Generator().manual_seed(1)).to(torch.bfloat16)
-    lin.forward(x, rows=rows)  # warm-up
-    ts = []
-    for _ in range(reps):
-        t = time.perf_counter()
-        lin.forward(x, rows=rows)
-        ts.append(time.perf_counter() - t)
-    ts.sort()
+    med, tot = timed(lambda: lin.forward(x, rows=rows), reps)
     frac = rows / d["out_f"]
-    med = ts[len(ts) // 2]
     gbs = alg_bytes_full * frac / med / 1e9
+    # decode only (the same tiles, no matmul)
+    def decode_only():
+        for i in range(0, rows, 1024):
+            lin.decode_tile(i, min(i + 1024, rows))   # each tile dropped, as forward() drops it
+
+    dmed, dtot = timed(decode_only, max(3, reps // 3))
+    # configuration 1: 2048x1536, whole weight
+    w1 = bench_weight(2048, 1536, seed=0)
+    d1 = bx.bf16x_quantize(w1)
+    lin1 = CpuBf16xLinear(d1, tile=1024)
+    c1med, c1tot = timed(lin1.decode_to_bf16, 5)
+    c1_bytes = sum(d1[k].numel() * d1[k].element_size() for k in ("sign_packed", "mant_packed", "delta_packed",
+                                                                    "emax", "delta_ovf_idx", "delta_ovf_val"))
+    # configuration 3 GEMM lines: M = 16 / 256 on the first 2048 rows
+    gemm = []
+    grows = min(2048, d["out_f"])
+    for M, n in ((16, 5), (256, 3)):
+        xm = torch.randn(M, d["in_f"], generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+        gmed, gtot = timed(lambda: lin.forward(xm, rows=grows), n)
+        gemm.append({"M": M, "rows": f"{grows} of {d['out_f']}", "seconds_per_sample": round(gmed, 4),
+                     "TFLOPs": round(2.0 * M * grows * d["in_f"] / gmed / 1e12, 6),
+                     "timed_s": round(gtot, 1)})
     cpu = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as f:
@@ -111,8 +168,15 @@ def cpu_baseline(d: dict, alg_bytes_full: int, rows: int, reps: int) -> dict:
         pass
     return {"value": round(gbs, 4), "unit": "GB/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"{rows} of {d['out_f']} rows (decode+matmul, batch 1), median of {reps} passes after 1 "
-                      f"warm-up, {sum(ts):.1f} s timed",
-            "seconds_per_sample": round(med, 4), "cpu": cpu}
+                      f"warm-up, {tot:.1f} s timed",
+            "seconds_per_sample": round(med, 4), "cpu": cpu,
+            "decode_only": {"value": round(alg_bytes_full * frac / dmed / 1e9, 4), "unit": "GB/s",
+                            "sample": f"{rows} of {d['out_f']} rows", "seconds_per_sample": round(dmed, 4),
+                            "timed_s": round(dtot, 1)},
+            "config1_decode_2048x1536": {"seconds": round(c1med, 4),
+                                         "GBps_compressed": round(c1_bytes / c1med / 1e9, 4),
+                                         "timed_s": round(c1tot, 1)},
+            "config3_gemm": gemm}
 
 
 def measured_traffic():
@@ -184,7 +248,7 @@ def bench_sweep(bx, dev, stream) -> dict:
                     e[f"{path}_tflops"] = round(flops / sg / 1e12, 1)
                 st_ = time_launches(lambda i: torch.nn.functional.linear(xm, wd), 30, 3, stream, queued=True)
                 e["torch_bf16_linear_us"] = round(st_ * 1e6, 2)
-                e["auto_mfma_frac"] = round(flops / (e["auto_us"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+                gemm_roofline(e, flops, out_f, in_f)
                 gemm_rec.append(e)
                 log(f"config3 gemm {e}")
                 del xm
@@ -267,7 +331,9 @@ def bench_gemm_case(bx, dev, stream, case: str, reps: int) -> dict:
     """One fused decode+GEMM case run `reps` times back to back (the
     workload of the kernel-trace and counter profiles of the GEMM kernels):
     dict = the packed dict of the configuration weights with its plan
-    (exact), gguf = GGUF blocks of Student-t (df 3) x 0.015 weights."""
+    (exact), gguf = GGUF blocks of Student-t (df 3) x 0.015 weights.  The
+    weight rotates over copies holding more than the Infinity Cache, so it
+    streams from HBM as in the benchmark lines."""
     import numpy as np
     fmt, shape, rows = case.split(":")
     out_f, in_f = (int(v) for v in shape.split("x"))
@@ -276,20 +342,32 @@ def bench_gemm_case(bx, dev, stream, case: str, reps: int) -> dict:
     if fmt == "dict":
         d = bx.bf16x_quantize(bench_weight(out_f, in_f, seed=0).to(dev))
         plan = bx.build_plan_host(d, device=dev)
-        plan.kplan()
-        fn = lambda i: bx.bf16x_gemm(xm, d["sign_packed"], d["mant_packed"], d["delta_packed"], d["emax"], out_f,
-                                     in_f, plan=plan, path="fused")
+        keys = ("sign_packed", "mant_packed", "delta_packed", "emax")
+        nc = max(2, -(-3 * MALL_BYTES // (sum(d[k].numel() * d[k].element_size() for k in keys) + plan.nbytes)))
+        cps = [({k: d[k].clone() for k in keys},
+                dataclasses.replace(plan, tile_off=plan.tile_off.clone(), tile_ent=plan.tile_ent.clone(),
+                                    tile_sat=plan.tile_sat.clone())) for _ in range(nc)]
+        for _, p in cps:
+            p.kplan()
+
+        def fn(i):
+            g, p = cps[i % nc]
+            bx.bf16x_gemm(xm, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                          plan=p, path="fused")
     elif fmt == "gguf":
         rng = np.random.default_rng(0)
         w = (rng.standard_t(3, size=(out_f, in_f)) * 0.015).astype(np.float32)
-        b = bx.gguf.device_blocks(bx.gguf.quantize_blocks(w), dev)
+        b0 = bx.gguf.device_blocks(bx.gguf.quantize_blocks(w), dev)
         del w
-        fn = lambda i: bx.gguf.gguf_gemm_fused(xm, b, out_f, in_f)
+        nc = max(2, -(-3 * MALL_BYTES // b0.numel()))
+        bs = [b0] + [b0.clone() for _ in range(nc - 1)]
+        fn = lambda i: bx.gguf.gguf_gemm_fused(xm, bs[i % nc], out_f, in_f)
     else:
         raise ValueError(f"unknown case format {fmt!r}")
     sec = time_launches(fn, reps, 2, stream)
     flops = 2.0 * M * out_f * in_f
-    return {"case": case, "reps": reps, "us": round(sec * 1e6, 2), "tflops": round(flops / sec / 1e12, 1),
+    return {"case": case, "reps": reps, "rotating_copies": nc, "us": round(sec * 1e6, 2),
+            "tflops": round(flops / sec / 1e12, 1),
             "mfma_frac": round(flops / sec / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
 
 
@@ -396,7 +474,7 @@ def main():
                     help="skip the configuration-2/3 shape sweep (GEMV at four shapes, GEMM at three x five M)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a 1 GiB device copy (counter calibration for rocprofv3 --pmc)")
-    ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 2048],
+    ap.add_argument("--gemm-rows", type=int, nargs="*", default=[16, 256, 512, 2048],
                     help="activation rows of the decode+GEMM lines (configuration 3)")
     ap.add_argument("--only", choices=("llama", "gguf", "sweep", "gemm"),
                     help="run one secondary workload alone and print its record (a measurement / profiling mode, "
@@ -532,12 +610,12 @@ def main():
                 bx.bf16x_gemm(xm, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
                               plan=p, path=path)
             n_l = max(6, min(60, int(0.05 / max(flops / 5e14, 1e-6))))
-            sec_g = time_launches(step_g, n_l, 3, stream)
+            sec_g = time_launches(step_g, n_l, 3, stream, queued=True)
             ent[f"{path}_us"] = round(sec_g * 1e6, 2)
             ent[f"{path}_tflops"] = round(flops / sec_g / 1e12, 1)
-        sec_t = time_launches(lambda i: torch.nn.functional.linear(xm, wd), 30, 3, stream)
+        sec_t = time_launches(lambda i: torch.nn.functional.linear(xm, wd), 30, 3, stream, queued=True)
         ent["torch_bf16_linear_us"] = round(sec_t * 1e6, 2)
-        ent["auto_mfma_frac"] = round(flops / (ent["auto_us"] * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)
+        gemm_roofline(ent, flops, out_f, in_f)
         gemm_rec.append(ent)
         log(f"gemm {ent}")
         del xm

@@ -77,7 +77,7 @@ def test_gemv_and_gemm(bx, shape):
 
 # fused decode + GEMM: ragged M (rows past M in a 256-row tile), ragged out_f
 # (rows past out_f in a 128-row tile), split K (few tiles) and whole K
-@pytest.mark.parametrize("shape", [(256, 4096), (1000, 1024), (200, 4224), (96, 28672)])
+@pytest.mark.parametrize("shape", [(256, 4096), (1000, 1024), (200, 4224), (96, 28672), (1100, 1024)])
 def test_gemm_fused(bx, shape):
     out_f, in_f = shape
     print("gguf gemm fused", shape, flush=True)
@@ -94,7 +94,8 @@ def test_gemm_fused(bx, shape):
             check_tol(y.float().cpu().numpy(), ref)
     # the dispatching entry, leading dims kept: one row (GEMV), the fused
     # GEMM's range, above it (decode + library GEMM)
-    for lead in ((1, 1), (3, 1), (2, 150), (1, bx.gguf.GGUF_GEMM_MAX_ROWS + 1)):
+    for lead in ((1, 1), (3, 1), (2, 150), (1, bx.gguf.GGUF_GEMM_MAX_ROWS_TALL + 1),
+                 (1, bx.gguf.GGUF_GEMM_MAX_ROWS + 1)):
         x3 = torch.randn(*lead, in_f, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
         y3 = bx.gguf.gguf_gemm(x3.to(DEV), b, out_f, in_f)
         assert y3.shape == (*lead, out_f) and y3.dtype == torch.bfloat16
