@@ -93,6 +93,8 @@ def gemm_kernel_name(M: int, out_f: int, in_f: int) -> str:
     if M <= 32:
         return "gemm_skinny_kernel"
     if M >= 192:
+        if (in_f // 64) % 4 == 0:
+            return "gemm_ws4_kernel (wave-specialised, 256-column groups, 32x32x16 MFMA)"
         return "gemm_ws_kernel (wave-specialised, 32x32x16 MFMA)"
     return "gemm_kernel (tiled)"
 

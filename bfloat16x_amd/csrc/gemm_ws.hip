@@ -384,6 +384,351 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   }
 }
 
+// ---------------------------------------------------------------------------
+// Four-step groups (in_f % 256 == 0): the kernel above with the W tile of one
+// barrier interval 256 columns wide (64 KB per slot, two slots), so that the
+// decode waves read runs of consecutive atoms of a row.  In round i (0..3)
+// lane l of decode wave 4 + p takes tile row 32p + 8i + l/8 and atom l%8 of
+// the group: a load instruction reads 8 rows x 8 consecutive atoms (368
+// contiguous bytes of a GGUF row, 224 of a mantissa stream) instead of 32
+// rows x 2 atoms, about 1.7x fewer cache lines per instruction (a timing copy
+// of the one-step kernel with this access pattern ran 11-24 % faster).  Each
+// round's registers are refilled with the next group's atoms as soon as they
+// are decoded, so one set of 4 rounds is in flight while the other is decoded.
+// Tile rows are 512 bytes; 16-byte chunk c of row r sits at
+// c ^ (((c >> 4) & 1) << 1) ^ (r & 15): the MFMA waves' reads (16 rows, one
+// chunk) and the decode waves' writes (2 rows x 8 atoms, one chunk of each)
+// each touch 16 different 16-byte bank groups.  The MFMA waves run the
+// one-step kernel's step four times per barrier.
+// ---------------------------------------------------------------------------
+constexpr int kGroup = 4;                    // 64-column steps per group
+constexpr int kRowB4 = kGroup * kRowB;       // 512 bytes per tile row
+constexpr int kWSlot4 = kBN * kRowB4;        // 64 KB
+
+__device__ __forceinline__ int swz4(int row, int chunk) { return chunk ^ (((chunk >> 4) & 1) << 1) ^ (row & 15); }
+
+template <bool GG, bool EXACT, bool PARTIAL, bool YF32>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_ws4_kernel(
+    const uint16_t* __restrict__ x, int64_t M, const uint32_t* __restrict__ sign,
+    const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
+    const uint8_t* __restrict__ blocks, const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent,
+    int64_t out_f, int64_t in_f, int groups_per_split, int mtiles, int ntiles, void* __restrict__ y) {
+  __shared__ __attribute__((aligned(16))) uint8_t wlds[2 * kWSlot4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // XCD-aware tile order, as gemm_ws_kernel
+  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
+  const int per = nb / 8, extra = nb - per * 8;
+  const int lb = nb >= 8 ? ((b & 7) * per + min(b & 7, extra) + (b >> 3)) : b;
+  const int64_t m0 = (int64_t)(lb % mtiles) * kBM;
+  const int nt = (lb / mtiles) % ntiles;
+  const int kb = lb / mtiles / ntiles;
+  const int64_t n0 = (int64_t)nt * kBN;
+  const int S = (int)(in_f >> 6);
+  const int SG = S / kGroup;
+  const int g0 = kb * groups_per_split;
+  const int ng = min(groups_per_split, SG - g0);   // groups of this block (>= 1)
+
+  if (wave >= 4) {
+    // ===================== decode waves =====================
+    const int pw = wave - 4;                    // 0..3
+    const int64_t P = in_f >> 5;                // atoms per row (a multiple of 8)
+    const int a = lane & 7, rq = lane >> 3;     // atom of the group, row within a round
+    using RawT = typename std::conditional<GG, RawG, Raw>::type;
+    const uint64_t wat = (uint64_t)(out_f - n0) * P;
+    __amdgpu_buffer_rsrc_t rs_, rm_, rd_, re_, rb_;
+    uint32_t vo_s = 0, vo_m = 0, vo_d = 0, vo_e = 0, vo_b = 0, sh = 0;
+    // round 0's atom from the tile's first atom; rows past out_f read zeros
+    // (buffer range check), their outputs are not stored
+    const uint32_t av = (uint32_t)((32 * pw + rq) * P) + (uint32_t)a;
+    const uint32_t rstep = (uint32_t)(8 * P);   // atoms from one round's row to the next
+    if constexpr (GG) {
+      // P is even, so block av sits at av * 46, which is 2 (a & 1) modulo 4
+      rb_ = rsrc(blocks + (uint64_t)n0 * P * 46, (wat * 46 + 3) & ~3ull);
+      vo_b = (av * 46) & ~3u;
+      sh = 16u * (uint32_t)(a & 1);
+    } else {
+      rs_ = rsrc(sign + n0 * P, wat * 4);
+      rm_ = rsrc(mant + n0 * P * 7, wat * 28);
+      rd_ = rsrc(delta + n0 * P * 3, wat * 12);
+      re_ = rsrc(emax2 + n0 * P, wat * 2);
+      vo_s = av * 4; vo_m = av * 28; vo_d = av * 12; vo_e = (av & ~1u) * 2;
+    }
+    // the atoms of round i of group gj (clamped to the block's last group)
+    auto load_round = [&](int gj, int i, RawT& t) {
+      const uint32_t ra = (uint32_t)(g0 + min(gj, ng - 1)) * 8u + (uint32_t)i * rstep;
+      if constexpr (GG) {
+        t.q0 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)vo_b, (int)(ra * 46), 0);
+        t.q1 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)(vo_b + 16), (int)(ra * 46), 0);
+        t.q2 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)(vo_b + 32), (int)(ra * 46), 0);
+      } else {
+        const u32x4 m03 = __builtin_amdgcn_raw_buffer_load_b128(rm_, (int)vo_m, (int)(ra * 28), 0);
+        const u32x3 m46 = __builtin_amdgcn_raw_buffer_load_b96(rm_, (int)(vo_m + 16), (int)(ra * 28), 0);
+        const u32x3 d02 = __builtin_amdgcn_raw_buffer_load_b96(rd_, (int)vo_d, (int)(ra * 12), 0);
+        t.s = __builtin_amdgcn_raw_buffer_load_b32(rs_, (int)vo_s, (int)(ra * 4), 0);
+        t.ew = __builtin_amdgcn_raw_buffer_load_b32(re_, (int)vo_e, (int)(ra * 2), 0);
+        const uint32_t c0 = m03.x, c1 = m03.y, c2 = m03.z, c3 = m03.w, c4 = m46.x, c5 = m46.y, c6 = m46.z;
+        t.m[0] = c0; t.m[1] = c1; t.m[2] = c2; t.m[3] = c3; t.m[4] = c4; t.m[5] = c5; t.m[6] = c6;
+        const uint32_t e0 = d02.x, e1 = d02.y, e2 = d02.z;
+        t.d[0] = e0; t.d[1] = e1; t.d[2] = e2;
+      }
+    };
+    auto store_round = [&](const RawT& w, int i, int slot) {
+      uint32_t p[16];
+      if constexpr (GG) {
+        decode_pairs<true>(gguf_atom(GgufRaw{w.q0, w.q1, w.q2, sh}), p);
+      } else {
+        Atom t;
+        t.s = w.s;
+#pragma unroll
+        for (int k = 0; k < 7; ++k) t.m[k] = w.m[k];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) t.d[k] = w.d[k];
+        t.e = (uint16_t)(w.ew >> (16 * (a & 1)));
+        decode_pairs(t, p);
+      }
+      uint32_t q[16];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        q[k] = perm(p[2 * k + 1], p[2 * k], 0x05040100u);      // elements 2k, 2k+1
+        q[8 + k] = perm(p[2 * k + 1], p[2 * k], 0x07060302u);  // elements 16+2k, 17+2k
+      }
+      const int r = 32 * pw + 8 * i + rq;
+      uint8_t* row = wlds + slot * kWSlot4 + r * kRowB4;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        *(u32x4*)(row + swz4(r, 4 * a + c) * 16) = u32x4{q[4 * c], q[4 * c + 1], q[4 * c + 2], q[4 * c + 3]};
+    };
+
+    // EXACT plan: the runs of this wave's 32-row group at the 4 steps of a group
+    const int64_t G = (out_f + 31) / 32, G2 = 2 * G;
+    const int64_t gr = min(n0 / 32 + pw, G);
+    uint32_t kp_total = 0;
+    if constexpr (EXACT) kp_total = kp_off[S * G2];
+    const __amdgpu_buffer_rsrc_t rent = rsrc(kp_ent, (uint64_t)kp_total * 4);
+    const __amdgpu_buffer_rsrc_t roff = rsrc(kp_off, ((uint64_t)S * G2 + 1) * 4);
+    const uint32_t ob = (uint32_t)(2 * gr) * 4, oe = (uint32_t)min(2 * gr + 2, G2) * 4;
+    struct Off { uint32_t beg[kGroup], end[kGroup]; };
+    struct Ent { uint32_t beg[kGroup], end[kGroup], e0[kGroup], e1[kGroup]; };
+    auto load_off = [&](int gj, Off& o) {
+      const uint32_t s0 = (uint32_t)(g0 + min(gj, ng - 1)) * kGroup;
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        o.beg[u] = __builtin_amdgcn_raw_buffer_load_b32(roff, (int)ob, (int)((s0 + u) * G2 * 4), 0);
+        o.end[u] = __builtin_amdgcn_raw_buffer_load_b32(roff, (int)oe, (int)((s0 + u) * G2 * 4), 0);
+      }
+    };
+    auto load_ent = [&](const Off& o, Ent& e) {
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        e.beg[u] = __builtin_amdgcn_readfirstlane(o.beg[u]);
+        e.end[u] = __builtin_amdgcn_readfirstlane(o.end[u]);
+        e.e0[u] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((e.beg[u] + lane) * 4), 0, 0);
+        e.e1[u] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((e.beg[u] + lane + 64) * 4), 0, 0);
+      }
+    };
+    // entry -> its bf16 in the group tile (step u of the group); the empty
+    // asm makes the compiler wait for the entry's load outside the branch
+    auto patch_one = [&](uint32_t e, int slot, int u, bool live) {
+      const int rr = (int)(e >> 22) & (kBN - 1), c = (int)(e >> 16) & 63;
+      const uint32_t dst =
+          (uint32_t)(slot * kWSlot4 + rr * kRowB4 + swz4(rr, 8 * u + (c >> 3)) * 16 + (c & 7) * 2);
+      __asm__ volatile("" : "+v"(e));
+      if (live) *(uint16_t*)(wlds + dst) = (uint16_t)(e & 0xFFFFu);
+    };
+    auto patch = [&](const Ent& e, int slot) {
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        patch_one(e.e0[u], slot, u, e.beg[u] + lane < e.end[u]);
+        patch_one(e.e1[u], slot, u, e.beg[u] + lane + 64 < e.end[u]);
+      }
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u)
+        for (uint32_t k = e.beg[u] + 128 + lane; k < e.end[u]; k += 64)   // dense runs (rare)
+          patch_one(kp_ent[k], slot, u, true);
+    };
+
+    RawT R[4];
+    Off O{};
+    Ent E{};
+    // prologue: group 0's plan offsets and entries and group 1's offsets,
+    // group 0's atoms; group 0 decoded round by round, each round's registers
+    // refilled with group 1's atoms; then group 1's entries and group 2's
+    // offsets.  The loads in flight at the loop entry are then 4 rounds of
+    // atoms, entries, offsets, as at the end of every iteration.
+    if constexpr (EXACT) load_off(0, O);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (EXACT) { load_ent(O, E); load_off(1, O); }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) load_round(0, i, R[i]);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      store_round(R[i], i, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_round(1, i, R[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (EXACT) {
+      patch(E, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_ent(O, E);
+      load_off(2, O);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+
+    // iteration j: group j + 1 decoded into slot (j + 1) & 1, round by round,
+    // each round's registers refilled with group j + 2's atoms; its plan
+    // entries patched, then group j + 2's entries and group j + 3's offsets
+    auto iter = [&](int j, int slot) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        store_round(R[i], i, slot);
+        __builtin_amdgcn_sched_barrier(0);
+        load_round(j + 2, i, R[i]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if constexpr (EXACT) {
+        patch(E, slot);
+        __builtin_amdgcn_sched_barrier(0);
+        load_ent(O, E);
+        load_off(j + 3, O);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      __syncthreads();
+    };
+    int j = 0;
+    for (; j + 1 < ng; j += 2) {
+      iter(j, 1);
+      iter(j + 1, 0);
+    }
+    if (j < ng) iter(j, 1);
+    return;
+  }
+
+  // ===================== MFMA waves =====================
+  const int lr = lane & 31, h = lane >> 5;
+  const int n = ng * kGroup;                  // steps of this block
+  const int s0 = g0 * kGroup;
+  const int64_t S64 = S;
+  const __amdgpu_buffer_rsrc_t rx_ = rsrc(x + m0 * in_f, (uint64_t)(((M + 31) / 32) * 32 - m0) * (uint64_t)in_f * 2);
+  const uint32_t vx0 = (uint32_t)(2 * wave * S64 * 4096 + lane * 16);
+  const uint32_t vx1 = vx0 + (uint32_t)(S64 * 4096);
+  auto load_x = [&](int jx, bf16x8_t (&X)[2][4]) {
+    const uint32_t ks = (uint32_t)(s0 + min(jx, n - 1)) * 4096;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rx_, (int)((i ? vx1 : vx0) + q * 1024), (int)ks, 0);
+        X[i][q] = __builtin_bit_cast(bf16x8_t, v);
+      }
+  };
+  // W operand of row tile jj, k-quarter q at step u of the group in slot
+  // `slot`: chunk 8u + 4h + q of row jj*32 + lr.  The chunk's swizzle splits
+  // into a per-lane part (wo[q]) and a constant of u, joined with one XOR;
+  // the slot is bit 16 of the address and jj an immediate offset.
+  uint32_t wo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) wo[q] = (uint32_t)(lr * kRowB4 + (((4 * h + q) ^ (lr & 15)) * 16));
+  auto load_w = [&](int q, int u, int slot, bf16x8_t (&wb)[4]) {
+    const uint32_t ku = (uint32_t)(((8 * u) ^ ((u >> 1) << 1)) * 16) | ((uint32_t)slot << 16);
+    const uint32_t o = wo[q] ^ ku;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) wb[jj] = *(const bf16x8_t*)(wlds + o + jj * 32 * kRowB4);
+  };
+  f32x16 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][jj][v] = 0.f;
+  auto mfma = [&](int t, const bf16x8_t (&X)[2][4], int q, const bf16x8_t (&wb)[4]) {
+    const int i = t >> 2, jj = t & 3;
+    acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(X[i][q], wb[jj], acc[i][jj], 0, 0, 0);
+  };
+#define BF16X_SG(mask, cnt) __builtin_amdgcn_sched_group_barrier(mask, cnt, 0)
+  bf16x8_t X0[2][4], X1[2][4], W0[4], W1[4];
+  // step u of the group in `slot` (block step jx) with x in X; x of step
+  // jx + 1 requested into Xn first.  The last quarter's second half reads
+  // the next step's quarter-0 W operands: after the group's barrier from the
+  // other slot at u == 3, from the same slot otherwise.
+  auto step = [&](int jx, int u, int slot, const bf16x8_t (&X)[2][4], bf16x8_t (&Xn)[2][4]) {
+    load_x(jx + 1, Xn);
+    load_w(1, u, slot, W1);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mfma(t, X, 0, W0);
+    BF16X_SG(0x020, 8);
+    BF16X_SG(0x100, 4);
+    BF16X_SG(0x008, 8);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(2, u, slot, W0);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mfma(t, X, 1, W1);
+    BF16X_SG(0x100, 4);
+    BF16X_SG(0x008, 8);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(3, u, slot, W1);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) mfma(t, X, 2, W0);
+    BF16X_SG(0x100, 4);
+    BF16X_SG(0x008, 8);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) mfma(t, X, 3, W1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (u == kGroup - 1) {
+      __syncthreads();
+      load_w(0, 0, slot ^ 1, W0);
+    } else {
+      load_w(0, u + 1, slot, W0);
+    }
+#pragma unroll
+    for (int t = 4; t < 8; ++t) mfma(t, X, 3, W1);
+    BF16X_SG(0x100, 4);
+    BF16X_SG(0x008, 4);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+#undef BF16X_SG
+  auto group = [&](int jg, int slot) {
+    step(4 * jg + 0, 0, slot, X0, X1);
+    step(4 * jg + 1, 1, slot, X1, X0);
+    step(4 * jg + 2, 2, slot, X0, X1);
+    step(4 * jg + 3, 3, slot, X1, X0);
+  };
+  load_x(0, X0);
+  __syncthreads();
+  load_w(0, 0, 0, W0);
+  int jg = 0;
+  for (; jg + 1 < ng; jg += 2) {
+    group(jg, 0);
+    group(jg + 1, 1);
+  }
+  if (jg < ng) group(jg, 0);
+
+  // ---- store: register v of lane l -> token row 8(v/4) + 4(l/32) + v%4, W row l%32
+  float* yp = (float*)y;
+  if constexpr (PARTIAL) yp += (int64_t)kb * M * out_f;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int64_t col = n0 + jj * 32 + lr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = m0 + wave * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (row < M && col < out_f) {
+          if constexpr (PARTIAL || YF32) yp[row * out_f + col] = acc[i][jj][v];
+          else ((uint16_t*)y)[row * out_f + col] = (uint16_t)f32_to_bf16_rne(acc[i][jj][v]);
+        }
+      }
+    }
+  }
+}
+
 // x [M, K] -> operand order: 32-row tile T, step s (64 columns), k-quarter q
 // is 1 KB at ((T * S + s) * 4 + q) * 1024, lane l = lr + 32 h holding row
 // 32 T + lr, columns 64 s + 32 h + 8 q .. +7 (the MFMA A operand of the
@@ -422,21 +767,26 @@ struct WsShape {
 // K is split while the tile count leaves CUs idle: the split minimises
 // (rounds of 256 resident blocks) x (steps per block), charging 10 % per
 // extra split (fp32 partials written and summed), smallest split on ties.
+// With four-step groups (S % 4 == 0) a split is a whole number of groups.
+bool ws_grouped(int64_t in_f) { return (in_f / kStep) % kGroup == 0; }
+
 WsShape ws_shape(int64_t M, int64_t out_f, int64_t in_f) {
   WsShape g;
   g.mtiles = (int)((M + kBM - 1) / kBM);
   g.ntiles = (int)((out_f + kBN - 1) / kBN);
   const int64_t S = in_f / kStep, tiles = (int64_t)g.mtiles * g.ntiles;
+  const int64_t gran = ws_grouped(in_f) ? kGroup : 1;
+  auto steps_of = [&](int64_t k) { return ((S + k - 1) / k + gran - 1) / gran * gran; };
   int best = 1;
   double best_cost = 1e30;
   for (int k = 1; k <= 16 && k * 4 <= S; ++k) {
-    const int64_t sps = (S + k - 1) / k, ks = (S + sps - 1) / sps;
+    const int64_t sps = steps_of(k), ks = (S + sps - 1) / sps;
     const double cost = (double)((tiles * ks + 255) / 256) * sps * (1.0 + 0.10 * (ks - 1));
     if (cost < best_cost - 1e-9) { best_cost = cost; best = (int)ks; }
   }
   const int64_t forced = tuning(BF16X_TUNE_GEMM_WS_SPLIT);
-  if (forced > 0) best = (int)std::min<int64_t>(forced, S);
-  g.sps = (int)((S + best - 1) / best);
+  if (forced > 0) best = (int)std::min<int64_t>(forced, S / gran);
+  g.sps = (int)steps_of(best);
   g.nsplit = (int)((S + g.sps - 1) / g.sps);
   return g;
 }
@@ -477,9 +827,18 @@ int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const 
   const uint16_t* xo = (const uint16_t*)workspace;
   float* part = (float*)((uint8_t*)workspace + xop);
   void* out = split ? (void*)part : y;
-#define BF16X_WS1(GG_, EX_, PA_, YF_)                                                                            \
-  hipLaunchKernelGGL((gemm_ws_kernel<GG_, EX_, PA_, YF_>), dim3((unsigned)grid), dim3(512), 0, st, xo, M, s, m, d, \
-                     e, blocks, kp_off, kp_ent, out_f, in_f, g.sps, g.mtiles, g.ntiles, out)
+  // four-step groups when K allows (the grouped kernel reads W in runs of
+  // consecutive atoms); BF16X_TUNE_GEMM_WS_GROUPED = 0 keeps the one-step kernel
+  const bool grouped = ws_grouped(in_f) && tuning(BF16X_TUNE_GEMM_WS_GROUPED) != 0;
+#define BF16X_WS1(GG_, EX_, PA_, YF_)                                                                             \
+  do {                                                                                                          \
+    if (grouped)                                                                                                \
+      hipLaunchKernelGGL((gemm_ws4_kernel<GG_, EX_, PA_, YF_>), dim3((unsigned)grid), dim3(512), 0, st, xo, M, s, \
+                         m, d, e, blocks, kp_off, kp_ent, out_f, in_f, g.sps / kGroup, g.mtiles, g.ntiles, out);    \
+    else                                                                                                        \
+      hipLaunchKernelGGL((gemm_ws_kernel<GG_, EX_, PA_, YF_>), dim3((unsigned)grid), dim3(512), 0, st, xo, M, s,  \
+                         m, d, e, blocks, kp_off, kp_ent, out_f, in_f, g.sps, g.mtiles, g.ntiles, out);             \
+  } while (0)
 #define BF16X_WS(GG_)                                        \
   do {                                                       \
     if (split) {                                             \

@@ -324,16 +324,22 @@ def _gemm_launch(x2, s, m, d, e, out_f, in_f, plan, y, y_dtype, sub=16):
 # and runs the product as a plain library GEMM (hipBLASLt through
 # F.linear): the decode is amortised over the rows and the library GEMM runs
 # closer to the MFMA peak than the fused kernel.  Below it the fused kernel
-# avoids writing and re-reading the decoded weight.  Weights with more columns
-# than rows switch at twice that many rows.  Measured (exact, rotated
-# weights): 14336x4096 M = 256: fused 72 us against 88 us, M = 384: 105
-# against 94 us; 4096x14336 M = 512: 112 against 127 us, M = 768: 172
-# against 147 us.
+# avoids writing and re-reading the decoded weight.  The switch depends on the
+# weight's shape (GEMM_DECODE_MIN_ROWS for square weights, _TALL for more rows
+# than columns, _WIDE for more columns than rows).  Measured (exact, rotated
+# weights, fused against decode + hipBLASLt): 4096x4096 M = 256: 34.8 against
+# 33.9 us, M = 384: 42.1 against 39.1 us; 14336x4096 M = 512: 90 against
+# 101 us, M = 768: 153 against 128 us; 4096x14336 M = 1024: 157 against
+# 166 us, M = 2048: 272 against 239 us.
 GEMM_DECODE_MIN_ROWS = 320
+GEMM_DECODE_MIN_ROWS_TALL = 640
+GEMM_DECODE_MIN_ROWS_WIDE = 1536
 
 
 def _decode_min_rows(out_f: int, in_f: int) -> int:
-    return 2 * GEMM_DECODE_MIN_ROWS if in_f > out_f else GEMM_DECODE_MIN_ROWS
+    if in_f > out_f:
+        return GEMM_DECODE_MIN_ROWS_WIDE
+    return GEMM_DECODE_MIN_ROWS_TALL if out_f > in_f else GEMM_DECODE_MIN_ROWS
 
 
 def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None = None, sub=16,
@@ -347,8 +353,8 @@ def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None =
     fp32) accumulated over two passes in fp32.
     path "decode": W decoded into a temporary by the HIP decoder, then
     F.linear on the same device (fp32 for fp16/fp32 activations).
-    path "auto": "decode" from GEMM_DECODE_MIN_ROWS rows on (twice that for
-    weights with more columns than rows) and for shapes the fused kernel does
+    path "auto": "decode" from GEMM_DECODE_MIN_ROWS rows on (_TALL / _WIDE for
+    weights with more rows / columns) and for shapes the fused kernel does
     not take (in_f not a multiple of 64, or above 65536), "fused" otherwise."""
     if path not in ("auto", "fused", "decode"):
         raise ValueError(f"path must be auto, fused or decode, not {path!r}")

@@ -163,3 +163,35 @@ def test_gemm_few_rows_identity_is_bit_exact(bx, M):
                               in_f, plan=p, path="fused")
             got = y.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)[:cols].T
             assert np.array_equal(got, ref[:, start:start + cols]), (start, p is None)
+
+
+# The wave-specialised kernel (M >= 192): four-step groups when in_f % 256 == 0
+# (grouped = 1, the default there) and one-step tiles otherwise or when forced
+# (grouped = 0); K splits forced to 1 and 3 (3 leaves a shorter last split).
+@pytest.mark.parametrize("grouped", [1, 0])
+@pytest.mark.parametrize("split", [-1, 1, 3])
+@pytest.mark.parametrize("M,out_f,in_f", [(300, 300, 4096), (192, 136, 1024), (260, 256, 3072)])
+def test_gemm_ws_groups_and_splits(bx, tune, grouped, split, M, out_f, in_f):
+    print("gemm ws", M, out_f, in_f, "grouped", grouped, "split", split, flush=True)
+    tune(gemm_ws_grouped=grouped, gemm_ws_split=split)
+    bits = dc.bench_weight_bits(out_f, in_f, seed=out_f + split)
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    dn = _np(d)
+    plan = bx.build_plan_host(d, device=DEV)
+    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M + split)).to(torch.bfloat16)
+    for p, sat in ((plan, False), (None, True)):
+        y = bx.bf16x_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                          plan=p, path="fused")
+        check_tol(y.float().cpu().numpy(), dc.gemm_ref(dn, x.float().numpy(), saturated=sat))
+    # the weight the kernel used, bit for bit: x = rows of I select W columns
+    eye = torch.zeros(M, in_f, dtype=torch.bfloat16)
+    cols = torch.arange(M) * (in_f // M)
+    eye[torch.arange(M), cols] = 1
+    w_cols = bx.bf16x_gemm(eye.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                           plan=plan, path="fused")
+    got = w_cols.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+    want = bits[:, cols.numpy()].T
+    flush = (want & 0x7F80) == 0                # zeros and subnormals (the MFMA flushes these) come back as 0
+    assert np.array_equal(np.where(flush, 0, got), np.where(flush, 0, want))
+    assert not np.any(got[flush] & 0x7FFF)

@@ -8,8 +8,9 @@ activations between kernels, and the accumulation order of each kernel
 (hipBLASLt for the bf16 linears, the fused decode+GEMV / GEMM kernels for
 BF16X).  The check is that BF16X adds no error of its own: its distance to
 fp32 is within 10 % of the bf16 stack's, position by position on average.
-Positions: the last token of three prefills (16, 28 and 40 tokens) and seven
-greedy decode steps after the 40-token prefill.  The greedy-agreement check of
+Positions: the last token of three prefills (16, 40 and 256 tokens: the
+few-row and the wave-specialised fused GEMMs) and seven greedy decode steps
+after the 256-token prefill.  The greedy-agreement check of
 the reference's harness (bench_fused_cpm5.py:96-100) compares the two stacks'
 tokens; here each stack is also measured against fp32 directly.
 """
@@ -24,8 +25,8 @@ from tests.test_gpu_dict import DEV
 
 pytestmark = pytest.mark.gpu
 
-PROMPT = 40
-PREFILLS = (16, 28, 40)
+PROMPT = 256
+PREFILLS = (16, 40, 256)      # the 256-token prefill runs the wave-specialised GEMM
 N_NEW = 8
 
 
