@@ -45,10 +45,12 @@
 //    bytes; 16-byte chunk c of row r sits at c ^ ((r >> 1) & 7), so 16 lanes
 //    reading one logical chunk of 16 consecutive rows touch 16 different
 //    16-byte bank groups (64 banks).
-//  * MFMA k-slots: in k-quarter q, lanes 0-31 hold columns 8q .. 8q+7 of the
-//    step and lanes 32-63 columns 32+8q .. 32+8q+7, for x (A operand) and W
-//    (B operand) alike.  Result register v of lane l is
-//    D[8(v/4) + 4(l/32) + v%4][l%32]: token row, W row.
+//  * MFMA k-slots: in k-quarter q, lanes 0-31 hold 8 columns of the step's
+//    first half and lanes 32-63 the same 8 of its second half, for x (A
+//    operand) and W (B operand) alike: columns 4q .. 4q+3 and 16+4q .. 19+4q
+//    of the half, interleaved (the order the decode leaves them in, see
+//    chunk_of).  Result register v of lane l is D[8(v/4) + 4(l/32) + v%4][l%32]:
+//    token row, W row.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -72,6 +74,16 @@ constexpr int kWSlot = kBN * kRowB;    // 16 KB
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
 
+// K order inside a 64-column step.  decode_pairs leaves element j of an atom
+// in the low half of word j and element 16 + j in the high half; W is stored
+// as decoded (no permute), so 16-byte chunk c of atom h (words 4c .. 4c+3)
+// holds atom columns 4c, 16+4c, 4c+1, 17+4c, 4c+2, 18+4c, 4c+3, 19+4c.  x_op
+// writes x's operand chunks in the same column order, so both MFMA operands
+// see one permutation of K.  Column c (0..63) of a step sits in chunk
+// chunk_of(c) of the step's 8, at bf16 position pos_of(c).
+__device__ __forceinline__ int chunk_of(int c) { return ((c >> 5) << 2) | ((c >> 2) & 3); }
+__device__ __forceinline__ int pos_of(int c) { return ((c & 3) << 1) | ((c >> 4) & 1); }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint64_t bytes) {
   const uint32_t n = bytes > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)bytes;
   return __builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)n, 0x00020000);
@@ -86,32 +98,102 @@ struct RawG {
   u32x4 q0, q1, q2;
 };
 
+// Block -> work.  Blocks [0, full) each own one output tile over all of K
+// (tiles 0 .. full-1); the remaining blocks split K for the last `ltiles`
+// tiles in `lunits`-unit ranges (units: steps, or four-step groups) and write
+// fp32 partials, summed by ws_tile_reduce_kernel.  full is a multiple of the
+// resident block count, so the split blocks fill the last round.  Within
+// each range the order is XCD-aware: blocks go round-robin over 8 XCDs, and
+// each XCD gets a contiguous run of tiles, M fastest, so the M tiles that
+// share a W tile run on one XCD at the same time and share its L2.
+struct WsGrid {
+  int mtiles, full, ltiles, lunits;
+};
+struct WsWork {
+  int64_t m0, n0;
+  int u0, nu;     // first unit and unit count of this block
+  int lt;         // split tile index (0 .. ltiles-1), or -1 for a full tile
+  int kb;         // K range of a split tile
+};
+__device__ __forceinline__ int xcd_order(int b, int nb) {
+  const int per = nb / 8, extra = nb - per * 8;
+  return nb >= 8 ? ((b & 7) * per + min(b & 7, extra) + (b >> 3)) : b;
+}
+__device__ __forceinline__ WsWork ws_work(const WsGrid& g, int units) {
+  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
+  WsWork w;
+  int tile;
+  if (b < g.full) {
+    tile = xcd_order(b, g.full);
+    w.lt = -1; w.kb = 0; w.u0 = 0; w.nu = units;
+  } else {
+    const int lb = xcd_order(b - g.full, nb - g.full);
+    w.lt = lb % g.ltiles; w.kb = lb / g.ltiles;
+    tile = g.full + w.lt;
+    w.u0 = w.kb * g.lunits;
+    w.nu = min(g.lunits, units - w.u0);
+  }
+  w.m0 = (int64_t)(tile % g.mtiles) * kBM;
+  w.n0 = (int64_t)(tile / g.mtiles) * kBN;
+  return w;
+}
+
+// The output tile from the MFMA waves' accumulators: register v of lane l ->
+// token row 8(v/4) + 4(l/32) + v%4, W row l%32.  A split tile's partial goes
+// to its own 256 x 128 fp32 tile of `part` (all of it: rows past M and
+// columns past out_f hold zeros), in K-range order.
+template <bool YF32>
+__device__ __forceinline__ void ws_store(const f32x16 (&acc)[2][4], const WsWork& w, int wave, int lane, int64_t M,
+                                         int64_t out_f, int ltiles, void* __restrict__ y, float* __restrict__ part) {
+  const int lr = lane & 31, h = lane >> 5;
+  if (w.lt >= 0) {
+    float* pt = part + ((int64_t)w.kb * ltiles + w.lt) * (kBM * kBN);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int r = wave * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+          pt[r * kBN + jj * 32 + lr] = acc[i][jj][v];
+        }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int64_t col = w.n0 + jj * 32 + lr;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = w.m0 + wave * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+        if (row < M && col < out_f) {
+          if constexpr (YF32) ((float*)y)[row * out_f + col] = acc[i][jj][v];
+          else ((uint16_t*)y)[row * out_f + col] = (uint16_t)f32_to_bf16_rne(acc[i][jj][v]);
+        }
+      }
+    }
+  }
+}
+
 // GG: W is GGUF half-blocks (`blocks`, 46 bytes per 32 elements, row-major;
 // the dict stream pointers are unused), decoded with the zero marker
 // (bf16x_gguf_block.py:76-87).  Otherwise W is the packed dict.
-template <bool GG, bool EXACT, bool PARTIAL, bool YF32>
+template <bool GG, bool EXACT, bool YF32>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_ws_kernel(
     const uint16_t* __restrict__ x, int64_t M, const uint32_t* __restrict__ sign,
     const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
     const uint8_t* __restrict__ blocks, const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent,
-    int64_t out_f, int64_t in_f, int steps_per_split, int mtiles, int ntiles, void* __restrict__ y) {
+    int64_t out_f, int64_t in_f, WsGrid grid, void* __restrict__ y, float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) uint8_t wlds[2 * kWSlot];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // XCD-aware tile order: blocks are dispatched round-robin over 8 XCDs; give
-  // each XCD a contiguous run of tiles, M fastest, so the M tiles that share a
-  // W tile run on one XCD at the same time and share its L2.
-  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
-  const int per = nb / 8, extra = nb - per * 8;
-  const int lb = nb >= 8 ? ((b & 7) * per + min(b & 7, extra) + (b >> 3)) : b;
-  const int64_t m0 = (int64_t)(lb % mtiles) * kBM;
-  const int nt = (lb / mtiles) % ntiles;
-  const int kb = lb / mtiles / ntiles;
-  const int64_t n0 = (int64_t)nt * kBN;
   const int S = (int)(in_f >> 6);
-  const int s0 = kb * steps_per_split;
-  const int n = min(steps_per_split, S - s0);   // steps of this block (>= 1)
+  const WsWork wk = ws_work(grid, S);           // units are steps
+  const int64_t m0 = wk.m0, n0 = wk.n0;
+  const int s0 = wk.u0;
+  const int n = wk.nu;                          // steps of this block (>= 1)
 
   if (wave >= 4) {
     // ===================== staging waves =====================
@@ -177,16 +259,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         t.e = (uint16_t)(w.ew >> (16 * a));
         decode_pairs(t, p);
       }
-      uint32_t q[16];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        q[i] = perm(p[2 * i + 1], p[2 * i], 0x05040100u);      // elements 2i, 2i+1
-        q[8 + i] = perm(p[2 * i + 1], p[2 * i], 0x07060302u);  // elements 16+2i, 17+2i
-      }
+      // chunk c = pairs 4c .. 4c+3 as decoded: K order kchunk(c), as x_op writes x
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         *(u32x4*)(wlds + wst + slot * kWSlot + swz(r, 4 * a + c) * 16) =
-            u32x4{q[4 * c], q[4 * c + 1], q[4 * c + 2], q[4 * c + 3]};
+            u32x4{p[4 * c], p[4 * c + 1], p[4 * c + 2], p[4 * c + 3]};
     };
 
     // EXACT plan: run of this wave's 32-row group at step s
@@ -216,7 +293,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // outstanding load.
     auto patch_one = [&](uint32_t e, int slot, bool live) {
       const int rr = (int)(e >> 22) & (kBN - 1), c = (int)(e >> 16) & 63;
-      const uint32_t dst = (uint32_t)(slot * kWSlot + rr * kRowB + swz(rr, c >> 3) * 16 + (c & 7) * 2);
+      const uint32_t dst = (uint32_t)(slot * kWSlot + rr * kRowB + swz(rr, chunk_of(c)) * 16 + pos_of(c) * 2);
       __asm__ volatile("" : "+v"(e));
       if (live) *(uint16_t*)(wlds + dst) = (uint16_t)(e & 0xFFFFu);
     };
@@ -363,25 +440,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     step(j + 1, 1, X1, X0);
   }
   if (j < n) step(j, 0, X0, X1);
-
-  // ---- store: register v of lane l -> token row 8(v/4) + 4(l/32) + v%4, W row l%32
-  float* yp = (float*)y;
-  if constexpr (PARTIAL) yp += (int64_t)kb * M * out_f;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int64_t col = n0 + jj * 32 + lr;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + wave * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (row < M && col < out_f) {
-          if constexpr (PARTIAL || YF32) yp[row * out_f + col] = acc[i][jj][v];
-          else ((uint16_t*)y)[row * out_f + col] = (uint16_t)f32_to_bf16_rne(acc[i][jj][v]);
-        }
-      }
-    }
-  }
+  ws_store<YF32>(acc, wk, wave, lane, M, out_f, grid.ltiles, y, part);
 }
 
 // ---------------------------------------------------------------------------
@@ -407,28 +466,21 @@ constexpr int kWSlot4 = kBN * kRowB4;        // 64 KB
 
 __device__ __forceinline__ int swz4(int row, int chunk) { return chunk ^ (((chunk >> 4) & 1) << 1) ^ (row & 15); }
 
-template <bool GG, bool EXACT, bool PARTIAL, bool YF32>
+template <bool GG, bool EXACT, bool YF32>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void gemm_ws4_kernel(
     const uint16_t* __restrict__ x, int64_t M, const uint32_t* __restrict__ sign,
     const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
     const uint8_t* __restrict__ blocks, const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent,
-    int64_t out_f, int64_t in_f, int groups_per_split, int mtiles, int ntiles, void* __restrict__ y) {
+    int64_t out_f, int64_t in_f, WsGrid grid, void* __restrict__ y, float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) uint8_t wlds[2 * kWSlot4];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // XCD-aware tile order, as gemm_ws_kernel
-  const int nb = (int)gridDim.x, b = (int)blockIdx.x;
-  const int per = nb / 8, extra = nb - per * 8;
-  const int lb = nb >= 8 ? ((b & 7) * per + min(b & 7, extra) + (b >> 3)) : b;
-  const int64_t m0 = (int64_t)(lb % mtiles) * kBM;
-  const int nt = (lb / mtiles) % ntiles;
-  const int kb = lb / mtiles / ntiles;
-  const int64_t n0 = (int64_t)nt * kBN;
   const int S = (int)(in_f >> 6);
-  const int SG = S / kGroup;
-  const int g0 = kb * groups_per_split;
-  const int ng = min(groups_per_split, SG - g0);   // groups of this block (>= 1)
+  const WsWork wk = ws_work(grid, S / kGroup);  // units are groups
+  const int64_t m0 = wk.m0, n0 = wk.n0;
+  const int g0 = wk.u0;
+  const int ng = wk.nu;                         // groups of this block (>= 1)
 
   if (wave >= 4) {
     // ===================== decode waves =====================
@@ -488,17 +540,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         t.e = (uint16_t)(w.ew >> (16 * (a & 1)));
         decode_pairs(t, p);
       }
-      uint32_t q[16];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        q[k] = perm(p[2 * k + 1], p[2 * k], 0x05040100u);      // elements 2k, 2k+1
-        q[8 + k] = perm(p[2 * k + 1], p[2 * k], 0x07060302u);  // elements 16+2k, 17+2k
-      }
       const int r = 32 * pw + 8 * i + rq;
       uint8_t* row = wlds + slot * kWSlot4 + r * kRowB4;
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        *(u32x4*)(row + swz4(r, 4 * a + c) * 16) = u32x4{q[4 * c], q[4 * c + 1], q[4 * c + 2], q[4 * c + 3]};
+        *(u32x4*)(row + swz4(r, 4 * a + c) * 16) = u32x4{p[4 * c], p[4 * c + 1], p[4 * c + 2], p[4 * c + 3]};
     };
 
     // EXACT plan: the runs of this wave's 32-row group at the 4 steps of a group
@@ -533,7 +579,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     auto patch_one = [&](uint32_t e, int slot, int u, bool live) {
       const int rr = (int)(e >> 22) & (kBN - 1), c = (int)(e >> 16) & 63;
       const uint32_t dst =
-          (uint32_t)(slot * kWSlot4 + rr * kRowB4 + swz4(rr, 8 * u + (c >> 3)) * 16 + (c & 7) * 2);
+          (uint32_t)(slot * kWSlot4 + rr * kRowB4 + swz4(rr, 8 * u + chunk_of(c)) * 16 + pos_of(c) * 2);
       __asm__ volatile("" : "+v"(e));
       if (live) *(uint16_t*)(wlds + dst) = (uint16_t)(e & 0xFFFFu);
     };
@@ -708,31 +754,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     group(jg + 1, 1);
   }
   if (jg < ng) group(jg, 0);
-
-  // ---- store: register v of lane l -> token row 8(v/4) + 4(l/32) + v%4, W row l%32
-  float* yp = (float*)y;
-  if constexpr (PARTIAL) yp += (int64_t)kb * M * out_f;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      const int64_t col = n0 + jj * 32 + lr;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + wave * 64 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-        if (row < M && col < out_f) {
-          if constexpr (PARTIAL || YF32) yp[row * out_f + col] = acc[i][jj][v];
-          else ((uint16_t*)y)[row * out_f + col] = (uint16_t)f32_to_bf16_rne(acc[i][jj][v]);
-        }
-      }
-    }
-  }
+  ws_store<YF32>(acc, wk, wave, lane, M, out_f, grid.ltiles, y, part);
 }
 
 // x [M, K] -> operand order: 32-row tile T, step s (64 columns), k-quarter q
 // is 1 KB at ((T * S + s) * 4 + q) * 1024, lane l = lr + 32 h holding row
-// 32 T + lr, columns 64 s + 32 h + 8 q .. +7 (the MFMA A operand of the
-// fused kernel).  Rows past M (up to the 32-row boundary) are zeros.  One
+// 32 T + lr, columns 64 s + 32 h + {4q, 16+4q, 4q+1, 17+4q, .., 4q+3, 19+4q}
+// (the MFMA A operand of the fused kernels, in the K order of the W tile).  Rows past M (up to the 32-row boundary) are zeros.  One
 // thread per 16-byte chunk, in output order.
 __global__ __launch_bounds__(256) void x_op_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t in_f,
                                                    int64_t chunks, u32x4* __restrict__ xo) {
@@ -741,54 +769,97 @@ __global__ __launch_bounds__(256) void x_op_kernel(const uint16_t* __restrict__ 
     const int l = (int)(c & 63), q = (int)((c >> 6) & 3);
     const int64_t ts = c >> 8, T = ts / S, s = ts - T * S;
     const int64_t row = T * 32 + (l & 31);
-    const int64_t col = s * 64 + (l >> 5) * 32 + q * 8;
+    const int64_t col = s * 64 + (l >> 5) * 32 + q * 4;   // columns col .. +3 and col+16 .. +19, interleaved
     u32x4 v = {0u, 0u, 0u, 0u};
-    if (row < M) v = *(const u32x4*)(x + row * in_f + col);
+    if (row < M) {
+      const u32x2a lo = *(const u32x2a*)(x + row * in_f + col), hi = *(const u32x2a*)(x + row * in_f + col + 16);
+      const uint32_t l0 = lo.x, l1 = lo.y, h0 = hi.x, h1 = hi.y;
+      v = u32x4{perm(h0, l0, 0x05040100u), perm(h0, l0, 0x07060302u), perm(h1, l1, 0x05040100u),
+                perm(h1, l1, 0x07060302u)};
+    }
     xo[c] = v;
   }
 }
 
-// y = sum over splits of the fp32 partials, in split order
+// y over the split tiles: the sum of each element's fp32 partials in K-range
+// order (partial tile layout as ws_store writes it).  One thread per element
+// of the split tiles' 256 x 128 partials, in order.
 template <bool YF32>
-__global__ __launch_bounds__(256) void ws_reduce_kernel(const float* __restrict__ ws, int64_t count, int nsplit,
-                                                        void* __restrict__ y) {
+__global__ __launch_bounds__(256) void ws_tile_reduce_kernel(const float* __restrict__ part, WsGrid g, int nsplit,
+                                                             int64_t M, int64_t out_f, void* __restrict__ y) {
+  const int64_t count = (int64_t)g.ltiles * (kBM * kBN);
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
-    float s = ws[i];
-    for (int k = 1; k < nsplit; ++k) s += ws[(int64_t)k * count + i];
-    if constexpr (YF32) ((float*)y)[i] = s;
-    else ((uint16_t*)y)[i] = (uint16_t)f32_to_bf16_rne(s);
+    const int lt = (int)(i / (kBM * kBN)), e = (int)(i % (kBM * kBN));
+    const int tile = g.full + lt;
+    const int64_t row = (int64_t)(tile % g.mtiles) * kBM + e / kBN;
+    const int64_t col = (int64_t)(tile / g.mtiles) * kBN + e % kBN;
+    if (row >= M || col >= out_f) continue;
+    float s = part[i];
+    for (int k = 1; k < nsplit; ++k) s += part[(int64_t)k * count + i];
+    if constexpr (YF32) ((float*)y)[row * out_f + col] = s;
+    else ((uint16_t*)y)[row * out_f + col] = (uint16_t)f32_to_bf16_rne(s);
   }
 }
 
 struct WsShape {
-  int mtiles, ntiles, nsplit, sps;
+  WsGrid g;
+  int nsplit;       // K ranges of a split tile (1: no split tiles)
+  int64_t grid;     // blocks
+  bool grouped;     // four-step-group kernel (units are groups, else steps)
 };
 
-// K is split while the tile count leaves CUs idle: the split minimises
-// (rounds of 256 resident blocks) x (steps per block), charging 10 % per
-// extra split (fp32 partials written and summed), smallest split on ties.
-// With four-step groups (S % 4 == 0) a split is a whole number of groups.
-bool ws_grouped(int64_t in_f) { return (in_f / kStep) % kGroup == 0; }
+// Four-step groups when K allows (the grouped kernel reads W in runs of
+// consecutive atoms); BF16X_TUNE_GEMM_WS_GROUPED = 0 keeps the one-step kernel.
+bool ws_grouped(int64_t in_f) {
+  return (in_f / kStep) % kGroup == 0 && tuning(BF16X_TUNE_GEMM_WS_GROUPED) != 0;
+}
 
+// Resident blocks of the wave-specialised kernels: one per CU (128 KB of LDS
+// and 8 waves of 256 registers each); 256 CUs when there is no device to ask.
+int64_t ws_resident() {
+  static int64_t cache[64];
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] > 0) return cache[dev];
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 256;
+  cache[dev] = cus;
+  return cus;
+}
+
+// Tiles run whole-K in full rounds of resident blocks; the f tiles of the
+// last, partial round (all tiles when there are fewer than one round) are
+// split into s = min(resident / f, 16) K ranges of at least one group (four
+// steps for the one-step kernel) so that they fill that round:
+// T = 896 tiles on 256 CUs run as 3 rounds of whole tiles and one round of
+// 128 tiles x 2 half-K blocks (3.5 rounds instead of 4), with fp32 partials
+// only for those 128 tiles.  BF16X_TUNE_GEMM_WS_SPLIT > 0 splits every tile
+// into that many K ranges instead; BF16X_TUNE_GEMM_WS_RESIDENT > 0 replaces
+// the resident block count (tests reach the mixed plan with few tiles).
 WsShape ws_shape(int64_t M, int64_t out_f, int64_t in_f) {
-  WsShape g;
-  g.mtiles = (int)((M + kBM - 1) / kBM);
-  g.ntiles = (int)((out_f + kBN - 1) / kBN);
-  const int64_t S = in_f / kStep, tiles = (int64_t)g.mtiles * g.ntiles;
-  const int64_t gran = ws_grouped(in_f) ? kGroup : 1;
-  auto steps_of = [&](int64_t k) { return ((S + k - 1) / k + gran - 1) / gran * gran; };
-  int best = 1;
-  double best_cost = 1e30;
-  for (int k = 1; k <= 16 && k * 4 <= S; ++k) {
-    const int64_t sps = steps_of(k), ks = (S + sps - 1) / sps;
-    const double cost = (double)((tiles * ks + 255) / 256) * sps * (1.0 + 0.10 * (ks - 1));
-    if (cost < best_cost - 1e-9) { best_cost = cost; best = (int)ks; }
-  }
+  WsShape w;
+  w.grouped = ws_grouped(in_f);
+  const int64_t mt = (M + kBM - 1) / kBM, nt = (out_f + kBN - 1) / kBN;
+  const int64_t S = in_f / kStep, tiles = mt * nt;
+  const int64_t units = w.grouped ? S / kGroup : S;
+  const int64_t max_split = std::max<int64_t>(1, std::min<int64_t>(16, w.grouped ? units : units / 4));
+  const int64_t forced_c = tuning(BF16X_TUNE_GEMM_WS_RESIDENT);
+  const int64_t C = forced_c > 0 ? forced_c : ws_resident();
+  int64_t f = tiles % C, s = f ? std::min<int64_t>(C / f, max_split) : 1;
   const int64_t forced = tuning(BF16X_TUNE_GEMM_WS_SPLIT);
-  if (forced > 0) best = (int)std::min<int64_t>(forced, S / gran);
-  g.sps = (int)steps_of(best);
-  g.nsplit = (int)((S + g.sps - 1) / g.sps);
-  return g;
+  if (forced > 0) {
+    f = tiles;
+    s = std::min<int64_t>(forced, w.grouped ? units : S);
+  }
+  const int64_t lunits = (units + s - 1) / s, ks = (units + lunits - 1) / lunits;
+  w.g.mtiles = (int)mt;
+  if (ks <= 1) {
+    w.g.full = (int)tiles; w.g.ltiles = 0; w.g.lunits = (int)units; w.nsplit = 1;
+    w.grid = tiles;
+  } else {
+    w.g.full = (int)(tiles - f); w.g.ltiles = (int)f; w.g.lunits = (int)lunits; w.nsplit = (int)ks;
+    w.grid = (tiles - f) + f * ks;
+  }
+  return w;
 }
 
 }  // namespace
@@ -802,8 +873,8 @@ int64_t ws_xop_bytes(int64_t M, int64_t in_f) { return ((M + 31) / 32) * 32 * in
 }  // namespace
 
 int64_t bf16x_gemm_ws_workspace(int64_t M, int64_t out_f, int64_t in_f) {
-  const WsShape g = ws_shape(M, out_f, in_f);
-  return ws_xop_bytes(M, in_f) + (g.nsplit > 1 ? (int64_t)g.nsplit * M * out_f * 4 : 0);
+  const WsShape w = ws_shape(M, out_f, in_f);
+  return ws_xop_bytes(M, in_f) + (w.nsplit > 1 ? (int64_t)w.nsplit * w.g.ltiles * (kBM * kBN) * 4 : 0);
 }
 
 // Launch of the wave-specialised kernel; arguments checked by the caller
@@ -813,58 +884,50 @@ int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const 
                          const uint16_t* e, const uint8_t* blocks, const uint32_t* kp_off, const uint32_t* kp_ent,
                          int64_t out_f, int64_t in_f, bool exact, bool yf32, void* y, void* workspace,
                          int64_t workspace_bytes, hipStream_t st) {
-  const WsShape g = ws_shape(M, out_f, in_f);
-  const bool split = g.nsplit > 1;
+  const WsShape w = ws_shape(M, out_f, in_f);
   const int64_t xop = ws_xop_bytes(M, in_f);
   if (!workspace || !aligned16(workspace) || workspace_bytes < bf16x_gemm_ws_workspace(M, out_f, in_f))
     return BF16X_ECAPACITY;
   if (xop >= (int64_t)0xFFFFFFFF) return BF16X_ESHAPE;
-  const int64_t grid = (int64_t)g.mtiles * g.ntiles * g.nsplit;
-  if (grid > INT32_MAX) return BF16X_ESHAPE;
+  if (w.grid > INT32_MAX) return BF16X_ESHAPE;
   const int64_t chunks = xop / 16;
   hipLaunchKernelGGL(x_op_kernel, dim3((unsigned)std::min<int64_t>((chunks + 255) / 256, 8192)), dim3(256), 0, st,
                      x, M, in_f, chunks, (u32x4*)workspace);
   const uint16_t* xo = (const uint16_t*)workspace;
   float* part = (float*)((uint8_t*)workspace + xop);
-  void* out = split ? (void*)part : y;
-  // four-step groups when K allows (the grouped kernel reads W in runs of
-  // consecutive atoms); BF16X_TUNE_GEMM_WS_GROUPED = 0 keeps the one-step kernel
-  const bool grouped = ws_grouped(in_f) && tuning(BF16X_TUNE_GEMM_WS_GROUPED) != 0;
-#define BF16X_WS1(GG_, EX_, PA_, YF_)                                                                             \
-  do {                                                                                                          \
-    if (grouped)                                                                                                \
-      hipLaunchKernelGGL((gemm_ws4_kernel<GG_, EX_, PA_, YF_>), dim3((unsigned)grid), dim3(512), 0, st, xo, M, s, \
-                         m, d, e, blocks, kp_off, kp_ent, out_f, in_f, g.sps / kGroup, g.mtiles, g.ntiles, out);    \
-    else                                                                                                        \
-      hipLaunchKernelGGL((gemm_ws_kernel<GG_, EX_, PA_, YF_>), dim3((unsigned)grid), dim3(512), 0, st, xo, M, s,  \
-                         m, d, e, blocks, kp_off, kp_ent, out_f, in_f, g.sps, g.mtiles, g.ntiles, out);             \
+  const dim3 grid((unsigned)w.grid);
+#define BF16X_WS1(GG_, EX_, YF_)                                                                                   \
+  do {                                                                                                           \
+    if (w.grouped)                                                                                               \
+      hipLaunchKernelGGL((gemm_ws4_kernel<GG_, EX_, YF_>), grid, dim3(512), 0, st, xo, M, s, m, d, e, blocks,       \
+                         kp_off, kp_ent, out_f, in_f, w.g, y, part);                                              \
+    else                                                                                                         \
+      hipLaunchKernelGGL((gemm_ws_kernel<GG_, EX_, YF_>), grid, dim3(512), 0, st, xo, M, s, m, d, e, blocks,        \
+                         kp_off, kp_ent, out_f, in_f, w.g, y, part);                                              \
   } while (0)
 #define BF16X_WS(GG_)                                        \
   do {                                                       \
-    if (split) {                                             \
-      if (exact) BF16X_WS1(GG_, true, true, false);          \
-      else BF16X_WS1(GG_, false, true, false);               \
-    } else if (exact) {                                      \
-      if (yf32) BF16X_WS1(GG_, true, false, true);           \
-      else BF16X_WS1(GG_, true, false, false);               \
+    if (exact) {                                             \
+      if (yf32) BF16X_WS1(GG_, true, true);                  \
+      else BF16X_WS1(GG_, true, false);                      \
     } else {                                                 \
-      if (yf32) BF16X_WS1(GG_, false, false, true);          \
-      else BF16X_WS1(GG_, false, false, false);              \
+      if (yf32) BF16X_WS1(GG_, false, true);                 \
+      else BF16X_WS1(GG_, false, false);                     \
     }                                                        \
   } while (0)
   if (blocks) BF16X_WS(true);
   else BF16X_WS(false);
 #undef BF16X_WS
 #undef BF16X_WS1
-  if (split) {
-    const int64_t count = M * out_f;
+  if (w.nsplit > 1) {
+    const int64_t count = (int64_t)w.g.ltiles * (kBM * kBN);
     const int64_t blocks_r = std::min<int64_t>((count + 255) / 256, 4096);
     if (yf32)
-      hipLaunchKernelGGL(ws_reduce_kernel<true>, dim3((unsigned)blocks_r), dim3(256), 0, st, (const float*)part,
-                         count, g.nsplit, y);
+      hipLaunchKernelGGL(ws_tile_reduce_kernel<true>, dim3((unsigned)blocks_r), dim3(256), 0, st,
+                         (const float*)part, w.g, w.nsplit, M, out_f, y);
     else
-      hipLaunchKernelGGL(ws_reduce_kernel<false>, dim3((unsigned)blocks_r), dim3(256), 0, st, (const float*)part,
-                         count, g.nsplit, y);
+      hipLaunchKernelGGL(ws_tile_reduce_kernel<false>, dim3((unsigned)blocks_r), dim3(256), 0, st,
+                         (const float*)part, w.g, w.nsplit, M, out_f, y);
   }
   return launch_status();
 }

@@ -323,7 +323,8 @@ enum {
   BF16X_TUNE_GGUF_ITERS = 14,      /* rows per wave of the GGUF long-row GEMV                     */
   BF16X_TUNE_ATTN_SPLIT = 15,      /* 1: decode attention always on the split-key kernel          */
   BF16X_TUNE_GEMM_WS_GROUPED = 16, /* 0: the wave-specialised GEMM in one-step (64-column) tiles   */
-  BF16X_TUNE_COUNT = 17
+  BF16X_TUNE_GEMM_WS_RESIDENT = 17,/* resident blocks the wave-specialised GEMM plans its rounds for */
+  BF16X_TUNE_COUNT = 18
 };
 int bf16x_set_tuning(int32_t key, int64_t value);
 /* Current value of a key (-1 = automatic; also returned for an unknown key). */

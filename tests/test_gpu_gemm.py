@@ -195,3 +195,28 @@ def test_gemm_ws_groups_and_splits(bx, tune, grouped, split, M, out_f, in_f):
     flush = (want & 0x7F80) == 0                # zeros and subnormals (the MFMA flushes these) come back as 0
     assert np.array_equal(np.where(flush, 0, got), np.where(flush, 0, want))
     assert not np.any(got[flush] & 0x7FFF)
+
+
+# Whole-K tiles in full rounds, then the last round's tiles split over K: with
+# the resident block count forced to 4 or 5, the 6 tiles of 300 x 300 run as
+# 4 whole tiles + 2 tiles x 2 K ranges, or 5 whole tiles + 1 tile x 5 ranges
+# (4 with four-step groups: 16 groups in ranges of 4); 520 rows x 200 columns
+# (6 tiles, 3 M tiles) with 4 resident leaves the split tiles in two M rows.
+@pytest.mark.parametrize("grouped", [1, 0])
+@pytest.mark.parametrize("resident", [4, 5])
+@pytest.mark.parametrize("M,out_f,in_f", [(300, 300, 4096), (520, 200, 1024)])
+def test_gemm_ws_mixed_rounds(bx, tune, grouped, resident, M, out_f, in_f):
+    print("gemm ws mixed", M, out_f, in_f, "grouped", grouped, "resident", resident, flush=True)
+    tune(gemm_ws_grouped=grouped, gemm_ws_resident=resident)
+    bits = dc.bench_weight_bits(out_f, in_f, seed=resident)
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    dn = _np(d)
+    plan = bx.build_plan_host(d, device=DEV)
+    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M + resident)).to(torch.bfloat16)
+    for p, sat in ((plan, False), (None, True)):
+        for dt in (torch.bfloat16, torch.float32):
+            y = bx.bf16x_gemm(x.to(DEV).to(dt), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"],
+                              out_f, in_f, plan=p, path="fused")
+            assert y.dtype == dt
+            check_tol(y.float().cpu().numpy(), dc.gemm_ref(dn, x.float().numpy(), saturated=sat))
