@@ -9,13 +9,15 @@ launch; consecutive steps rotate over distinct copies of the compressed
 weight totalling more than twice the 256 MB Infinity Cache, so each launch
 streams its weight from HBM.  Inputs are resident in HBM before timing.
 
-value = algorithmic bytes per launch / mean launch time (HIP events on the
-launch stream), where algorithmic bytes =
+value = algorithmic bytes per launch / mean launch time over back-to-back
+launches (HIP events on the launch stream; gemv_single_launch adds the
+median over 200 launches timed one by one), where algorithmic bytes =
 4*(|sign|+|mant|+|delta|) + |emax| + 5*n_fix + 2*in_f + 2*out_f.
 Secondary fields (same rotation): the exact decode kernel's time and
 read+write bandwidth, and decode+GEMM (configuration 3) at --gemm-rows
 activation rows through the fused kernel ("fused") and the default dispatch
-("auto": fused below 256 rows, decode + hipBLASLt from 256 rows on), with
+("auto": fused below a shape-dependent row count, 640 for this tall weight,
+decode + hipBLASLt from there on), with
 torch bf16 F.linear on the decoded weight beside them; and configuration 5
 (GGUF half-block, 8192x28672 and 28672x8192, Student-t(3) x 0.015): fused
 decode+GEMV, decode, decode+GEMM at M = 512, clamped fraction and max abs
@@ -547,6 +549,20 @@ def main():
     sec = time_launches(step, args.steps, args.warmup, stream)
     gbs = abytes / sec / 1e9
     log(f"bf16x gemv: {sec * 1e6:.2f} us/launch, {gbs:.1f} GB/s algorithmic ({n_copies} rotating copies)")
+    # the same launches one at a time, each between its own pair of events:
+    # median and spread over 200 (the per-launch statistic; `value` is the
+    # back-to-back mean above)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(200)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record(stream)
+        step(i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    per = sorted(e0.elapsed_time(e1) * 1e3 for e0, e1 in evs)
+    single_rec = {"launches": len(per), "median_us": round(per[len(per) // 2], 2),
+                  "p10_us": round(per[len(per) // 10], 2), "p90_us": round(per[9 * len(per) // 10], 2),
+                  "median_GBps": round(abytes / (per[len(per) // 2] * 1e-6) / 1e9, 1)}
+    log(f"bf16x gemv, one launch per event pair: {single_rec}")
 
     if args.calib_copy:
         # a plain device copy of known size (1 GiB read, 1 GiB written) for
@@ -664,6 +680,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic()},
         "cpu_baseline": cpu,
+        "gemv_single_launch": single_rec,
         "bf16_gemv_us": round(sec_bf16 * 1e6, 3),
         "speedup_vs_bf16_gemv": round(sec_bf16 / sec, 3),
         "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 2),

@@ -88,6 +88,26 @@ def test_lossless_gemv_gemm(g, kind, shape):
             check_tol(y.cpu().numpy(), xm.double().numpy() @ wb.T)
 
 
+# Whole-K tiles in full rounds and the last round's tiles split over K (the
+# resident block count forced to 4): 520 x 300 rows x columns is 3 x 3 = 9
+# tiles, run as 8 whole tiles and one tile in 4 K ranges, with the table's
+# plan (lossless) and without it.
+@pytest.mark.parametrize("kind,shape", [("dense", (300, 4096)), ("selftest", (300, 1024))])
+def test_gemm_fused_mixed_rounds(g, tune, kind, shape):
+    print("gguf gemm mixed rounds", kind, shape, flush=True)
+    tune(gemm_ws_resident=4)
+    w = weights(kind, shape, 9)
+    wb = go.bf16_bits_to_fp32(go.fp32_to_bf16_bits(w)).astype(np.float64).reshape(shape)
+    packed = g.quantize_blocks(w)
+    wnl = go.dequantize_blocks(packed).astype(np.float64).reshape(shape)
+    t = g.device_ovf(g.pack_ovf(w), packed, DEV)
+    blocks = g.device_blocks(packed, DEV)
+    xm = torch.randn(520, shape[1], generator=torch.Generator().manual_seed(11)).to(torch.bfloat16)
+    for ovf, ref in ((t, wb), (None, wnl)):
+        y = g.gguf_gemm_fused(xm.to(DEV), blocks, *shape, out_dtype=torch.float32, ovf=ovf)
+        check_tol(y.cpu().numpy(), xm.double().numpy() @ ref.T)
+
+
 def test_tampered_table_refused(g):
     from bfloat16x_amd import _lib
     w = selftest_weights((16, 256), 8)
