@@ -472,7 +472,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
     const uint8_t* __restrict__ blocks, const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent,
     int64_t out_f, int64_t in_f, WsGrid grid, void* __restrict__ y, float* __restrict__ part) {
-  __shared__ __attribute__((aligned(16))) uint8_t wlds[2 * kWSlot4];
+  // two W slots, then 256 bytes where the plan patch lanes with no entry write
+  __shared__ __attribute__((aligned(16))) uint8_t wlds[2 * kWSlot4 + 256];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
@@ -574,25 +575,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         e.e1[u] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((e.beg[u] + lane + 64) * 4), 0, 0);
       }
     };
-    // entry -> its bf16 in the group tile (step u of the group); the empty
-    // asm makes the compiler wait for the entry's load outside the branch
+    // entry -> its bf16 in the group tile (step u of the group); a lane past
+    // the run writes its own word of the spare area instead (no exec-mask
+    // branch); the empty asm makes the compiler wait for the entry's load
+    // there
     auto patch_one = [&](uint32_t e, int slot, int u, bool live) {
       const int rr = (int)(e >> 22) & (kBN - 1), c = (int)(e >> 16) & 63;
       const uint32_t dst =
           (uint32_t)(slot * kWSlot4 + rr * kRowB4 + swz4(rr, 8 * u + chunk_of(c)) * 16 + pos_of(c) * 2);
       __asm__ volatile("" : "+v"(e));
-      if (live) *(uint16_t*)(wlds + dst) = (uint16_t)(e & 0xFFFFu);
+      *(uint16_t*)(wlds + (live ? dst : (uint32_t)(2 * kWSlot4 + lane * 4))) = (uint16_t)(e & 0xFFFFu);
     };
+    // the first 64 entries of each step's run; runs longer than 64 (rare)
+    // behind one uniform branch
     auto patch = [&](const Ent& e, int slot) {
+      uint32_t longest = 0;
 #pragma unroll
       for (int u = 0; u < kGroup; ++u) {
         patch_one(e.e0[u], slot, u, e.beg[u] + lane < e.end[u]);
-        patch_one(e.e1[u], slot, u, e.beg[u] + lane + 64 < e.end[u]);
+        longest = max(longest, e.end[u] - e.beg[u]);
       }
+      if (longest > 64) {
 #pragma unroll
-      for (int u = 0; u < kGroup; ++u)
-        for (uint32_t k = e.beg[u] + 128 + lane; k < e.end[u]; k += 64)   // dense runs (rare)
-          patch_one(kp_ent[k], slot, u, true);
+        for (int u = 0; u < kGroup; ++u) {
+          if (e.beg[u] + lane + 64 < e.end[u]) patch_one(e.e1[u], slot, u, true);
+          for (uint32_t k = e.beg[u] + 128 + lane; k < e.end[u]; k += 64)   // dense runs
+            patch_one(kp_ent[k], slot, u, true);
+        }
+      }
     };
 
     RawT R[4];
@@ -760,24 +770,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // x [M, K] -> operand order: 32-row tile T, step s (64 columns), k-quarter q
 // is 1 KB at ((T * S + s) * 4 + q) * 1024, lane l = lr + 32 h holding row
 // 32 T + lr, columns 64 s + 32 h + {4q, 16+4q, 4q+1, 17+4q, .., 4q+3, 19+4q}
-// (the MFMA A operand of the fused kernels, in the K order of the W tile).  Rows past M (up to the 32-row boundary) are zeros.  One
-// thread per 16-byte chunk, in output order.
+// (the MFMA A operand of the fused kernels, in the K order of the W tile).
+// Rows past M (up to the 32-row boundary) are zeros.  One thread per
+// (T, s, l): it reads the 64 contiguous bytes of its row's 32 columns (lanes
+// l and l + 32 take the two halves of a 128-byte row segment) and writes its
+// 16 bytes of each of the 4 k-quarters (each a contiguous 1 KB per wave).
 __global__ __launch_bounds__(256) void x_op_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t in_f,
-                                                   int64_t chunks, u32x4* __restrict__ xo) {
+                                                   int64_t units, u32x4* __restrict__ xo) {
   const int64_t S = in_f / 64;
-  for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < chunks; c += (int64_t)gridDim.x * 256) {
-    const int l = (int)(c & 63), q = (int)((c >> 6) & 3);
-    const int64_t ts = c >> 8, T = ts / S, s = ts - T * S;
+  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units; u += (int64_t)gridDim.x * 256) {
+    const int l = (int)(u & 63);
+    const int64_t ts = u >> 6, T = ts / S, s = ts - T * S;
     const int64_t row = T * 32 + (l & 31);
-    const int64_t col = s * 64 + (l >> 5) * 32 + q * 4;   // columns col .. +3 and col+16 .. +19, interleaved
-    u32x4 v = {0u, 0u, 0u, 0u};
+    uint32_t w[16] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
     if (row < M) {
-      const u32x2a lo = *(const u32x2a*)(x + row * in_f + col), hi = *(const u32x2a*)(x + row * in_f + col + 16);
-      const uint32_t l0 = lo.x, l1 = lo.y, h0 = hi.x, h1 = hi.y;
-      v = u32x4{perm(h0, l0, 0x05040100u), perm(h0, l0, 0x07060302u), perm(h1, l1, 0x05040100u),
-                perm(h1, l1, 0x07060302u)};
+      const u32x4a* src = (const u32x4a*)(x + row * in_f + s * 64 + (l >> 5) * 32);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const u32x4a v = src[c];
+        const uint32_t v0 = v.x, v1 = v.y, v2 = v.z, v3 = v.w;
+        w[4 * c] = v0; w[4 * c + 1] = v1; w[4 * c + 2] = v2; w[4 * c + 3] = v3;
+      }
     }
-    xo[c] = v;
+    // quarter q: columns 4q .. 4q+3 (words 2q, 2q+1) and 16+4q .. 19+4q (words 8+2q, 9+2q)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      xo[(ts * 4 + q) * 64 + l] = u32x4{perm(w[8 + 2 * q], w[2 * q], 0x05040100u),
+                                        perm(w[8 + 2 * q], w[2 * q], 0x07060302u),
+                                        perm(w[9 + 2 * q], w[2 * q + 1], 0x05040100u),
+                                        perm(w[9 + 2 * q], w[2 * q + 1], 0x07060302u)};
   }
 }
 
@@ -890,9 +911,9 @@ int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const 
     return BF16X_ECAPACITY;
   if (xop >= (int64_t)0xFFFFFFFF) return BF16X_ESHAPE;
   if (w.grid > INT32_MAX) return BF16X_ESHAPE;
-  const int64_t chunks = xop / 16;
-  hipLaunchKernelGGL(x_op_kernel, dim3((unsigned)std::min<int64_t>((chunks + 255) / 256, 8192)), dim3(256), 0, st,
-                     x, M, in_f, chunks, (u32x4*)workspace);
+  const int64_t units = xop / 64;   // (32-row tile, step, lane): 4 chunks of 16 bytes each
+  hipLaunchKernelGGL(x_op_kernel, dim3((unsigned)std::min<int64_t>((units + 255) / 256, 8192)), dim3(256), 0, st,
+                     x, M, in_f, units, (u32x4*)workspace);
   const uint16_t* xo = (const uint16_t*)workspace;
   float* part = (float*)((uint8_t*)workspace + xop);
   const dim3 grid((unsigned)w.grid);
