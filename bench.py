@@ -331,13 +331,15 @@ def bench_gguf(bx, dev, stream) -> list:
     return out
 
 
-def bench_gemm_case(bx, dev, stream, case: str, reps: int) -> dict:
-    """One fused decode+GEMM case run `reps` times back to back (the
-    workload of the kernel-trace and counter profiles of the GEMM kernels):
-    dict = the packed dict of the configuration weights with its plan
-    (exact), gguf = GGUF blocks of Student-t (df 3) x 0.015 weights.  The
-    weight rotates over copies holding more than the Infinity Cache, so it
-    streams from HBM as in the benchmark lines."""
+def bench_gemm_case(bx, dev, stream, case: str, reps: int, path: str = "fused") -> dict:
+    """One decode+GEMM case run `reps` times back to back (the workload of
+    the kernel-trace and counter profiles of the GEMM kernels): dict = the
+    packed dict of the configuration weights with its plan (exact), gguf =
+    GGUF blocks of Student-t (df 3) x 0.015 weights.  path "fused" runs the
+    fused kernel; "decode" (dict only) decodes W into a temporary and runs
+    F.linear (hipBLASLt), the default dispatch from a few hundred rows on.
+    The weight rotates over copies holding more than the Infinity Cache, so
+    it streams from HBM as in the benchmark lines."""
     import numpy as np
     fmt, shape, rows = case.split(":")
     out_f, in_f = (int(v) for v in shape.split("x"))
@@ -357,8 +359,10 @@ def bench_gemm_case(bx, dev, stream, case: str, reps: int) -> dict:
         def fn(i):
             g, p = cps[i % nc]
             bx.bf16x_gemm(xm, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
-                          plan=p, path="fused")
+                          plan=p, path=path)
     elif fmt == "gguf":
+        if path != "fused":
+            raise ValueError("--path decode takes a dict case")
         rng = np.random.default_rng(0)
         w = (rng.standard_t(3, size=(out_f, in_f)) * 0.015).astype(np.float32)
         b0 = bx.gguf.device_blocks(bx.gguf.quantize_blocks(w), dev)
@@ -370,7 +374,7 @@ def bench_gemm_case(bx, dev, stream, case: str, reps: int) -> dict:
         raise ValueError(f"unknown case format {fmt!r}")
     sec = time_launches(fn, reps, 2, stream)
     flops = 2.0 * M * out_f * in_f
-    return {"case": case, "reps": reps, "rotating_copies": nc, "us": round(sec * 1e6, 2),
+    return {"case": case, "path": path, "reps": reps, "rotating_copies": nc, "us": round(sec * 1e6, 2),
             "tflops": round(flops / sec / 1e12, 1),
             "mfma_frac": round(flops / sec / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
 
@@ -485,6 +489,8 @@ def main():
                          "not the benchmark line); gemm: one fused decode+GEMM case (--case) --steps times")
     ap.add_argument("--case", default="dict:14336x4096:512",
                     help="--only gemm case, FORMAT:OUTxIN:M with FORMAT dict (exact, packed dict) or gguf")
+    ap.add_argument("--path", choices=("fused", "decode"), default="fused",
+                    help="--only gemm: the fused kernel, or decode + F.linear (dict cases)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no multi-GPU path",
@@ -497,7 +503,7 @@ def main():
         st_ = torch.cuda.current_stream(dev)
         rec = (bench_llama(bx, dev) if args.only == "llama" else
                bench_gguf(bx, dev, st_) if args.only == "gguf" else
-               bench_gemm_case(bx, dev, st_, args.case, args.steps) if args.only == "gemm" else
+               bench_gemm_case(bx, dev, st_, args.case, args.steps, args.path) if args.only == "gemm" else
                bench_sweep(bx, dev, st_))
         print(json.dumps({"only": args.only, "record": rec}), flush=True)
         return

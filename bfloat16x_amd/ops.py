@@ -323,15 +323,17 @@ def _gemm_launch(x2, s, m, d, e, out_f, in_f, plan, y, y_dtype, sub=16):
 # From this many activation rows on, bf16x_gemm decodes W once at HBM speed
 # and runs the product as a plain library GEMM (hipBLASLt through
 # F.linear): the decode is amortised over the rows and the library GEMM runs
-# closer to the MFMA peak than the fused kernel.  Below it the fused kernel
-# avoids writing and re-reading the decoded weight.  The switch depends on the
-# weight's shape (GEMM_DECODE_MIN_ROWS for square weights, _TALL for more rows
-# than columns, _WIDE for more columns than rows).  Measured (exact, rotated
-# weights, fused against decode + hipBLASLt): 4096x4096 M = 256: 34.8 against
-# 33.9 us, M = 384: 42.1 against 39.1 us; 14336x4096 M = 512: 90 against
-# 101 us, M = 768: 153 against 128 us; 4096x14336 M = 1024: 157 against
-# 166 us, M = 2048: 272 against 239 us.
-GEMM_DECODE_MIN_ROWS = 320
+# closer to the MFMA peak than the fused kernel, which decodes every W tile
+# once per 256 activation rows (at 2048 rows, eight times).  Below it the
+# fused kernel avoids writing and re-reading the decoded weight.  The switch
+# depends on the weight's shape (GEMM_DECODE_MIN_ROWS for square weights,
+# _TALL for more rows than columns, _WIDE for more columns than rows).
+# Measured (exact, weights rotated through HBM, fused against decode +
+# hipBLASLt, us): 4096x4096 M = 512 / 640 / 768: 42.4 / 53.9 / 54.7 against
+# 54.0 / 53.9 / 52.3; 14336x4096 M = 512 / 640: 81.6 / 125.4 against
+# 102.9 / 115.7; 28672x4096 M = 512 / 640: 165.9 / 234.3 against 179.2 /
+# 218.8; 4096x14336 M = 1024 / 1536: 159.4 / 262.6 against 171.5 / 207.8.
+GEMM_DECODE_MIN_ROWS = 704
 GEMM_DECODE_MIN_ROWS_TALL = 640
 GEMM_DECODE_MIN_ROWS_WIDE = 1536
 
