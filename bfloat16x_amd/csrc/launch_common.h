@@ -16,6 +16,7 @@ inline int64_t tuning(int key) { return bf16x_tuning_value(key); }
 
 inline bool aligned2(const void* p) { return ((uintptr_t)p & 1u) == 0; }
 inline bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
+inline bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Status of the launch just enqueued: 0 or the hipError_t (> 0).

@@ -633,6 +633,183 @@ extern "C" int bf16x_rope_kv(const uint16_t* qkv, int64_t tokens, const int32_t*
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// Causal GQA attention for many query rows (prefill) on bf16 MFMA
+// (v_mfma_f32_16x16x32_bf16), flash-attention style: workgroup (query tile
+// of 64 rows, head h), 4 waves, wave w owns queries t0 + 16 w .. + 15; K and
+// V of the KV head stream through LDS in blocks of 32 keys (double
+// buffered, one barrier per block) and every query keeps a running softmax.
+// Same results as attention_kernel up to fp32 summation order: scores are
+// exact bf16 products summed in fp32 and scaled after the sum, the
+// probabilities enter P.V as two bf16 terms (hi + lo, 16 significant bits)
+// and the output is divided by the fp32 sum once, at the end.
+// Operand layout of the 16x16x32 MFMA (lane l, g = l / 16): A[l % 16][8 g +
+// v'], B[8 g + v'][l % 16], D register v = D[4 g + v][l % 16].  Both
+// products are computed transposed so that lane l always serves query
+// l % 16:
+//  * S^T = K Q^T: A = K rows (16 keys x 32 dims) from LDS, B = Q^T from
+//    registers (the query row's 8 dims of the chunk); lane l then holds the
+//    scores of keys 4 g + v (and 16 + 4 g + v) for its query;
+//  * O^T = V^T P^T: B = P^T straight from those registers (k slot 8 g + v'
+//    = key 4 g + v' for v' < 4, key 16 + 4 g + v' - 4 otherwise), A = V^T
+//    read from a transposed copy of the V block in LDS whose columns are in
+//    that slot order; lane l accumulates dims 16 dt + 4 g + v of its query.
+// LDS rows are padded (K: 272 bytes, V^T: 80 bytes) so that the 16 lanes of
+// an operand read touch 16 different 16-byte bank groups.
+namespace {
+constexpr int kFaQ = 64;                  // query rows per workgroup
+constexpr int kFaMinTokens = 16;          // bf16x_attention takes this kernel from this many rows on
+constexpr int kFaK = 32;                  // keys per block
+constexpr int kFaKRow = 272;              // bytes per K row in LDS (256 + 16)
+constexpr int kFaVRow = 80;               // bytes per V^T row in LDS (64 + 16)
+
+typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
+typedef float fa_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int fa_slot(int key) {   // V^T column of key 0..31
+  return key < 16 ? 8 * (key >> 2) + (key & 3) : 8 * ((key - 16) >> 2) + 4 + (key & 3);
+}
+
+__global__ __launch_bounds__(256) void attention_mfma_kernel(const uint16_t* __restrict__ q,
+                                                             const uint16_t* __restrict__ kc,
+                                                             const uint16_t* __restrict__ vc,
+                                                             const int32_t* __restrict__ pos, int T, int H, int KV,
+                                                             int max_len, float scale, uint16_t* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint8_t ks[2][kFaK * kFaKRow];
+  __shared__ __attribute__((aligned(16))) uint8_t vts[2][128 * kFaVRow];
+  const int t0 = (int)blockIdx.x * kFaQ, h = (int)blockIdx.y;
+  const int kvh = h / (H / KV);
+  const int tid = threadIdx.x, lane = tid & 63, gl = lane >> 4, ql = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int p0 = pos[0];
+  const int t = t0 + 16 * w + ql;                              // this lane's query row
+  const int pq = p0 + t;                                       // its position: keys 0 .. pq
+  const int nq = t < T ? max(0, min(pq + 1, max_len)) : 0;     // keys this query sees
+  const int tlast = min(t0 + kFaQ - 1, T - 1);
+  const int nmax = max(0, min(p0 + tlast + 1, max_len));       // keys any query of the tile sees
+  const int nblk = (nmax + kFaK - 1) / kFaK;
+
+  // Q^T operands: chunk c = dims 32 c + 8 gl .. + 7 of the lane's query
+  fa_bf16x8 qb[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (t < T) v = *(const u32x4*)(q + ((int64_t)t * H + h) * 128 + 32 * c + 8 * gl);
+    qb[c] = __builtin_bit_cast(fa_bf16x8, v);
+  }
+
+  // staging: thread (key tid / 8, 32-byte part tid % 8) of K, (dims 8 (tid % 16) .. +7, keys 2 (tid / 16), +1) of V
+  const uint16_t* K = kc + (int64_t)kvh * max_len * 128;
+  const uint16_t* V = vc + (int64_t)kvh * max_len * 128;
+  const int kk = tid >> 3, kp = tid & 7, vd = tid & 15, vk = 2 * (tid >> 4);
+  u32x4 kr[2], vr[2];
+  auto load_block = [&](int b) {
+    const int last = nmax - 1;                                 // rows past the context: a valid row (masked)
+    const uint16_t* kp_ = K + (int64_t)min(kFaK * b + kk, last) * 128 + 16 * kp;
+    kr[0] = *(const u32x4*)kp_;
+    kr[1] = *(const u32x4*)(kp_ + 8);
+    vr[0] = *(const u32x4*)(V + (int64_t)min(kFaK * b + vk, last) * 128 + 8 * vd);
+    vr[1] = *(const u32x4*)(V + (int64_t)min(kFaK * b + vk + 1, last) * 128 + 8 * vd);
+  };
+  auto store_block = [&](int slot) {
+    uint8_t* kd = ks[slot] + kk * kFaKRow + 32 * kp;
+    *(u32x4*)kd = kr[0];
+    *(u32x4*)(kd + 16) = kr[1];
+    const uint32_t a[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w}, b[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+    uint8_t* vd_ = vts[slot] + (8 * vd) * kFaVRow + 2 * fa_slot(vk);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      *(uint32_t*)(vd_ + (2 * e) * kFaVRow) = (a[e] & 0xFFFFu) | (b[e] << 16);
+      *(uint32_t*)(vd_ + (2 * e + 1) * kFaVRow) = (a[e] >> 16) | (b[e] & 0xFFFF0000u);
+    }
+  };
+
+  float m = -INFINITY, l = 0.f;
+  fa_f32x4 o[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = fa_f32x4{0.f, 0.f, 0.f, 0.f};
+
+  if (nblk > 0) {
+    load_block(0);
+    store_block(0);
+    if (nblk > 1) load_block(1);
+  }
+  __syncthreads();
+  for (int b = 0; b < nblk; ++b) {
+    const int slot = b & 1;
+    if (b + 1 < nblk) {
+      store_block(slot ^ 1);                                   // its last readers passed the previous barrier
+      if (b + 2 < nblk) load_block(b + 2);
+    }
+    // S^T = K Q^T for keys 32 b + 16 kt + (0 .. 15)
+    fa_f32x4 sacc[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      sacc[kt] = fa_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const fa_bf16x8 a =
+            *(const fa_bf16x8*)(ks[slot] + (16 * kt + ql) * kFaKRow + 64 * c + 16 * gl);
+        sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qb[c], sacc[kt], 0, 0, 0);
+      }
+    }
+    // running softmax of the lane's query over the block (its 8 keys here,
+    // the other 24 in lanes ql + 16, + 32, + 48)
+    float sv[8];
+    float mb = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int j = kFaK * b + 16 * kt + 4 * gl + v;
+        const float sc = j < nq ? sacc[kt][v] * scale : -INFINITY;
+        sv[4 * kt + v] = sc;
+        mb = fmaxf(mb, sc);
+      }
+    mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+    mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+    const float mn = fmaxf(m, mb);
+    const float alpha = mn == -INFINITY ? 1.f : __expf(m - mn);
+    float ps = 0.f;
+    uint32_t phi[4], plo[4];
+#pragma unroll
+    for (int k = 0; k < 8; k += 2) {
+      const float e0 = sv[k] == -INFINITY ? 0.f : __expf(sv[k] - mn);
+      const float e1 = sv[k + 1] == -INFINITY ? 0.f : __expf(sv[k + 1] - mn);
+      ps += e0 + e1;
+      const uint32_t h0 = f32_to_bf16_rne(e0), h1 = f32_to_bf16_rne(e1);
+      phi[k >> 1] = h0 | (h1 << 16);
+      plo[k >> 1] = f32_to_bf16_rne(e0 - bfv(h0)) | (f32_to_bf16_rne(e1 - bfv(h1)) << 16);
+    }
+    ps += __shfl_xor(ps, 16, 64);
+    ps += __shfl_xor(ps, 32, 64);
+    l = l * alpha + ps;
+    m = mn;
+    const fa_bf16x8 bhi = __builtin_bit_cast(fa_bf16x8, u32x4{phi[0], phi[1], phi[2], phi[3]});
+    const fa_bf16x8 blo = __builtin_bit_cast(fa_bf16x8, u32x4{plo[0], plo[1], plo[2], plo[3]});
+    // O^T = alpha O^T + V^T P^T
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      o[dt] *= alpha;
+      const fa_bf16x8 a = *(const fa_bf16x8*)(vts[slot] + (16 * dt + ql) * kFaVRow + 16 * gl);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bhi, o[dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, blo, o[dt], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+  if (t < T) {
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* op = out + ((int64_t)t * H + h) * 128 + 4 * gl;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const uint32_t lo = f32_to_bf16_rne(o[dt][0] * inv) | (f32_to_bf16_rne(o[dt][1] * inv) << 16);
+      const uint32_t hi = f32_to_bf16_rne(o[dt][2] * inv) | (f32_to_bf16_rne(o[dt][3] * inv) << 16);
+      *(uint2*)(op + 16 * dt) = make_uint2(lo, hi);
+    }
+  }
+}
+}  // namespace
+
 extern "C" int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                const int32_t* pos, int64_t tokens, int64_t n_heads, int64_t n_kv_heads,
                                int64_t head_dim, int64_t max_len, float scale, uint16_t* out,
@@ -643,6 +820,18 @@ extern "C" int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const
     return BF16X_ESHAPE;
   if (!aligned16(k_cache) || !aligned4(v_cache) || !aligned2(q) || !aligned2(out)) return BF16X_EARG;
   if (tokens == 0) return BF16X_OK;
+  // many query rows: the MFMA kernel (from kFaMinTokens rows, or as the
+  // override BF16X_TUNE_ATTN_MFMA says: 0 never, 1 always)
+  // (it loads q and V rows 16 bytes at a time and stores 8-byte runs of out)
+  const int64_t mf = tuning(BF16X_TUNE_ATTN_MFMA);
+  const bool mf_aligned = aligned16(q) && aligned16(v_cache) && aligned8(out);
+  if (mf == 1 && !mf_aligned) return BF16X_EARG;
+  if (mf == 1 || (mf != 0 && tokens >= kFaMinTokens && mf_aligned)) {
+    hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)((tokens + kFaQ - 1) / kFaQ), (unsigned)n_heads),
+                       dim3(256), 0, (hipStream_t)stream, q, k_cache, v_cache, pos, (int)tokens, (int)n_heads,
+                       (int)n_kv_heads, (int)max_len, scale, out);
+    return launch_status();
+  }
   hipLaunchKernelGGL(attention_kernel, dim3((unsigned)n_heads, (unsigned)tokens), dim3(256),
                      (size_t)max_len * sizeof(float), (hipStream_t)stream, q, k_cache, v_cache, pos, (int)n_heads,
                      (int)n_kv_heads, (int)max_len, scale, out);
@@ -657,7 +846,11 @@ extern "C" int bf16x_attention(const uint16_t* q, const uint16_t* k_cache, const
 // block of 128 keys, so it wins up to ~256 keys (measured: 1 key 5.8 vs
 // 9.9 us, 300 keys 10.8 vs 12.7, 600 keys 16.6 vs 13.7).
 // Keys are taken in blocks of 128, wave w keys 16w .. 16w+15 of a block, four
-// lanes per key for the scores (32 dims each) and lane l dims 2l, 2l+1 for
+// lanes per key for the scores (lane q of a key holds 16-byte chunk q of
+// each 64-byte quarter of the row, dims 32c + 8q .. 32c + 8q + 7: each K
+// load instruction then reads 64 contiguous bytes of each of its 16 keys,
+// half the cache-line accesses of a lane-per-quarter layout; measured
+// 13.3 -> 11.6 us per launch at 600 keys) and lane l dims 2l, 2l+1 for
 // P.V.  Each wave keeps a running softmax (max, sum, unnormalised output per
 // head) over its keys; K and V of the next block are in flight while a block
 // is processed.  At the end the 8 waves' states are combined in LDS in wave
@@ -692,10 +885,13 @@ __global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __
   __shared__ float wm[W][G], wl[W][G];     // per wave: running max and sum
   __shared__ float wacc[W][G][128];        // per wave: unnormalised output
   // PH: workgroup = query head hq of KV head g (G == 1); else workgroup = KV head g, query heads g G + h
+  // PH: block b serves query head (b % KV) gq + b / KV, so the gq workgroups
+  // of a KV head are KV blocks apart: with KV = 8 they run on one XCD
+  // (blocks go round-robin over the 8 XCDs) and share its L2 for the K / V rows
   const int gq = H / KV;
-  const int g = PH ? (int)blockIdx.x / gq : (int)blockIdx.x;
-  const int hq0 = PH ? (int)blockIdx.x : g * G;
-  const bool writer = !PH || (int)blockIdx.x % gq == 0;   // appends the new K / V row
+  const int g = PH ? (int)blockIdx.x % KV : (int)blockIdx.x;
+  const int hq0 = PH ? g * gq + (int)blockIdx.x / KV : g * G;
+  const bool writer = !PH || (int)blockIdx.x < KV;         // appends the new K / V row
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = lane >> 2, q4 = lane & 3;
@@ -713,9 +909,9 @@ __global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __
   int jmax = jmax_entry;
   auto load_k = [&](int b, u32x4 (&kr)[4]) {
     const int j = min(kBlock * b + 16 * w + kg, jmax);
-    const int off = j * 256 + 64 * q4;
+    const int off = j * 256 + 16 * q4;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) kr[c] = __builtin_amdgcn_raw_buffer_load_b128(rk, off + 16 * c, 0, 0);
+    for (int c = 0; c < 4; ++c) kr[c] = __builtin_amdgcn_raw_buffer_load_b128(rk, off + 64 * c, 0, 0);
   };
   auto load_v = [&](int b, uint32_t (&vr)[16]) {
 #pragma unroll
@@ -798,7 +994,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __
     }
     if (j >= n_old) {                                            // the new key (j == p), or past the end
 #pragma unroll
-      for (int e = 0; e < 16; ++e) kw[e] = kp2[16 * q4 + e];
+      for (int e = 0; e < 16; ++e) kw[e] = kp2[16 * (e >> 2) + 4 * q4 + (e & 3)];
     }
     float sc[G];
 #pragma unroll
@@ -807,7 +1003,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __
     for (int c = 0; c < 4; ++c) {
 #pragma unroll
       for (int h = 0; h < G; ++h) {
-        const u32x4 qv = *(const u32x4*)&qs2[h][16 * q4 + 4 * c];
+        const u32x4 qv = *(const u32x4*)&qs2[h][16 * c + 4 * q4];
         const uint32_t q0 = qv.x, q1 = qv.y, q2 = qv.z, q3 = qv.w;
         sc[h] = dot2_bf16(kw[4 * c], q0, sc[h]);
         sc[h] = dot2_bf16(kw[4 * c + 1], q1, sc[h]);

@@ -324,7 +324,8 @@ enum {
   BF16X_TUNE_ATTN_SPLIT = 15,      /* 1: decode attention always on the split-key kernel          */
   BF16X_TUNE_GEMM_WS_GROUPED = 16, /* 0: the wave-specialised GEMM in one-step (64-column) tiles   */
   BF16X_TUNE_GEMM_WS_RESIDENT = 17,/* resident blocks the wave-specialised GEMM plans its rounds for */
-  BF16X_TUNE_COUNT = 18
+  BF16X_TUNE_ATTN_MFMA = 18,       /* prefill attention: 0 the scalar kernel, 1 the MFMA kernel       */
+  BF16X_TUNE_COUNT = 19
 };
 int bf16x_set_tuning(int32_t key, int64_t value);
 /* Current value of a key (-1 = automatic; also returned for an unknown key). */

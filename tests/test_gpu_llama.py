@@ -154,6 +154,49 @@ def test_attention(bx, T, pos, L):
     assert float((err - (BF_ULP * ref.abs() + 1e-4)).max()) <= 0, float(err.max())
 
 
+def attn_ref_batched(q, kc, vc, pos, H, KV):
+    """attn_ref with the causal mask as one masked matrix product per head
+    (fp32 scores, fp64 softmax): q [T, H, 128], caches [KV, L, 128]."""
+    T, L = q.shape[0], kc.shape[1]
+    out = torch.zeros(T, H, 128)
+    qpos = pos + torch.arange(T)
+    keep = torch.arange(L)[None, :] <= qpos[:, None]                    # [T, L]
+    for h in range(H):
+        kvh = h // (H // KV)
+        s = (q[:, h] @ kc[kvh].t()) / math.sqrt(128)                     # [T, L]
+        s = s.double().masked_fill(~keep, float("-inf"))
+        p = torch.softmax(s, 1).float()
+        p = torch.nan_to_num(p)                                            # rows without keys
+        out[:, h] = p @ vc[kvh]
+    return out
+
+
+@torch.no_grad()
+@pytest.mark.parametrize("T,pos,L,H,KV", [(1, 0, 16, 8, 2), (7, 10, 64, 8, 2), (64, 0, 64, 8, 2),
+                                          (100, 3, 128, 8, 2), (16, 0, 48, 4, 4), (65, 959, 1024, 8, 1),
+                                          (512, 0, 640, 32, 8), (200, 300, 640, 32, 8)])
+def test_attention_mfma(bx, tune, T, pos, L, H, KV):
+    """The MFMA prefill kernel (forced with attn_mfma = 1, which the default
+    dispatch takes from 16 query rows) against an fp32 reference with the
+    causal mask, at full and ragged 64-row tiles, key counts that are not a
+    multiple of the 32-key block, several GQA groupings and the prefill
+    shape of the Llama harness; and against the scalar kernel."""
+    tune(attn_mfma=1)
+    q = rnd((T, H, 128), 21)
+    kc, vc = rnd((KV, L, 128), 22), rnd((KV, L, 128), 23)
+    p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    out = torch.empty(T, H * 128, dtype=torch.bfloat16, device=DEV)
+    llama.attention(q.to(DEV).view(T, H * 128), kc.to(DEV), vc.to(DEV), p, H, KV, out)
+    ref = attn_ref_batched(q.float(), kc.float(), vc.float(), pos, H, KV)
+    err = (out.float().cpu().view(T, H, 128) - ref).abs()
+    # fp32 softmax and sums, one bf16 rounding of the output
+    assert float((err - (BF_ULP * ref.abs() + 1e-4)).max()) <= 0, float(err.max())
+    with bx.tuning(attn_mfma=0):
+        out0 = torch.empty_like(out)
+        llama.attention(q.to(DEV).view(T, H * 128), kc.to(DEV), vc.to(DEV), p, H, KV, out0)
+    within_ulps(out, out0, 1.0, floor=1e-4)
+
+
 @torch.no_grad()
 @pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("H,KV,pos,L", [(4, 4, 0, 16), (8, 4, 5, 64), (32, 8, 300, 640), (32, 8, 639, 640),
