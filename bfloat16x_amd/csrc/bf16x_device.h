@@ -225,6 +225,14 @@ __device__ __forceinline__ Atom gguf_atom(const GgufRaw& r) {
 }
 
 __device__ __forceinline__ float bf16lo_to_f32(uint32_t p) { return __uint_as_float(p << 16); }
+
+// bf16(lo) | bf16(hi) << 16 rounded to nearest even (the default rounding
+// mode): one v_cvt_pk_bf16_f32 on gfx950.  Used where the inputs are finite
+// products of finite bf16 values, for which it gives f32_to_bf16_rne's bits.
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{lo, hi}), bf16x2_t));
+}
 __device__ __forceinline__ float bf16hi_to_f32(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
 
 __device__ __forceinline__ float dot2_bf16(uint32_t w, uint32_t x, float acc) {

@@ -351,14 +351,15 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
       tot = (nred[0] + nred[1]) + (nred[2] + nred[3]);
     }
     const float sc = 1.0f / sqrtf(tot / (float)in_f + na.eps);
+    // bf16(bf16(h * s) * w) per pair, each rounding one v_cvt_pk_bf16_f32
+    // (round to nearest even, as f32_to_bf16_rne for finite values)
 #pragma unroll
     for (int i = 0; i < XSLOTS; ++i)
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
         const uint32_t h = xs_reg[i][k], w = wn_reg[i][k];
-        const float lo = bf16lo_to_f32(f32_to_bf16_rne(bf16lo_to_f32(h) * sc)) * bf16lo_to_f32(w);
-        const float hi = bf16lo_to_f32(f32_to_bf16_rne(bf16hi_to_f32(h) * sc)) * bf16hi_to_f32(w);
-        xs_reg[i][k] = f32_to_bf16_rne(lo) | (f32_to_bf16_rne(hi) << 16);
+        const uint32_t hs = pk_bf16(bf16lo_to_f32(h) * sc, bf16hi_to_f32(h) * sc);
+        xs_reg[i][k] = pk_bf16(bf16lo_to_f32(hs) * bf16lo_to_f32(w), bf16hi_to_f32(hs) * bf16hi_to_f32(w));
       }
   }
 #pragma unroll
