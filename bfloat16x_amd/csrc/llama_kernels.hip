@@ -662,6 +662,7 @@ constexpr int kFaMinTokens = 16;          // bf16x_attention takes this kernel f
 constexpr int kFaK = 32;                  // keys per block
 constexpr int kFaKRow = 272;              // bytes per K row in LDS (256 + 16)
 constexpr int kFaVRow = 80;               // bytes per V^T row in LDS (64 + 16)
+constexpr int kFaD = 4;                   // key blocks in flight in registers
 
 typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
 typedef float fa_f32x4 __attribute__((ext_vector_type(4)));
@@ -702,20 +703,22 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const uint16_t* __r
   const uint16_t* K = kc + (int64_t)kvh * max_len * 128;
   const uint16_t* V = vc + (int64_t)kvh * max_len * 128;
   const int kk = tid >> 3, kp = tid & 7, vd = tid & 15, vk = 2 * (tid >> 4);
-  u32x4 kr[2], vr[2];
-  auto load_block = [&](int b) {
+  // key blocks in flight in registers: block k is loaded into set k % kFaD
+  // kFaD iterations before it is staged in LDS (one iteration before its use)
+  u32x4 kr[kFaD][2], vr[kFaD][2];
+  auto load_block = [&](int b, u32x4 (&k2)[2], u32x4 (&v2)[2]) {
     const int last = nmax - 1;                                 // rows past the context: a valid row (masked)
     const uint16_t* kp_ = K + (int64_t)min(kFaK * b + kk, last) * 128 + 16 * kp;
-    kr[0] = *(const u32x4*)kp_;
-    kr[1] = *(const u32x4*)(kp_ + 8);
-    vr[0] = *(const u32x4*)(V + (int64_t)min(kFaK * b + vk, last) * 128 + 8 * vd);
-    vr[1] = *(const u32x4*)(V + (int64_t)min(kFaK * b + vk + 1, last) * 128 + 8 * vd);
+    k2[0] = *(const u32x4*)kp_;
+    k2[1] = *(const u32x4*)(kp_ + 8);
+    v2[0] = *(const u32x4*)(V + (int64_t)min(kFaK * b + vk, last) * 128 + 8 * vd);
+    v2[1] = *(const u32x4*)(V + (int64_t)min(kFaK * b + vk + 1, last) * 128 + 8 * vd);
   };
-  auto store_block = [&](int slot) {
+  auto store_block = [&](int slot, const u32x4 (&k2)[2], const u32x4 (&v2)[2]) {
     uint8_t* kd = ks[slot] + kk * kFaKRow + 32 * kp;
-    *(u32x4*)kd = kr[0];
-    *(u32x4*)(kd + 16) = kr[1];
-    const uint32_t a[4] = {vr[0].x, vr[0].y, vr[0].z, vr[0].w}, b[4] = {vr[1].x, vr[1].y, vr[1].z, vr[1].w};
+    *(u32x4*)kd = k2[0];
+    *(u32x4*)(kd + 16) = k2[1];
+    const uint32_t a[4] = {v2[0].x, v2[0].y, v2[0].z, v2[0].w}, b[4] = {v2[1].x, v2[1].y, v2[1].z, v2[1].w};
     uint8_t* vd_ = vts[slot] + (8 * vd) * kFaVRow + 2 * fa_slot(vk);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -729,18 +732,7 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const uint16_t* __r
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) o[dt] = fa_f32x4{0.f, 0.f, 0.f, 0.f};
 
-  if (nblk > 0) {
-    load_block(0);
-    store_block(0);
-    if (nblk > 1) load_block(1);
-  }
-  __syncthreads();
-  for (int b = 0; b < nblk; ++b) {
-    const int slot = b & 1;
-    if (b + 1 < nblk) {
-      store_block(slot ^ 1);                                   // its last readers passed the previous barrier
-      if (b + 2 < nblk) load_block(b + 2);
-    }
+  auto compute = [&](int b, int slot) {
     // S^T = K Q^T for keys 32 b + 16 kt + (0 .. 15)
     fa_f32x4 sacc[2];
 #pragma unroll
@@ -777,9 +769,8 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const uint16_t* __r
       const float e0 = sv[k] == -INFINITY ? 0.f : __expf(sv[k] - mn);
       const float e1 = sv[k + 1] == -INFINITY ? 0.f : __expf(sv[k + 1] - mn);
       ps += e0 + e1;
-      const uint32_t h0 = f32_to_bf16_rne(e0), h1 = f32_to_bf16_rne(e1);
-      phi[k >> 1] = h0 | (h1 << 16);
-      plo[k >> 1] = f32_to_bf16_rne(e0 - bfv(h0)) | (f32_to_bf16_rne(e1 - bfv(h1)) << 16);
+      phi[k >> 1] = pk_bf16(e0, e1);
+      plo[k >> 1] = pk_bf16(e0 - bf16lo_to_f32(phi[k >> 1]), e1 - bf16hi_to_f32(phi[k >> 1]));
     }
     ps += __shfl_xor(ps, 16, 64);
     ps += __shfl_xor(ps, 32, 64);
@@ -795,7 +786,32 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const uint16_t* __r
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bhi, o[dt], 0, 0, 0);
       o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, blo, o[dt], 0, 0, 0);
     }
-    __syncthreads();
+  };
+
+  if (nblk > 0) {
+#pragma unroll
+    for (int d = 0; d < kFaD; ++d)
+      if (d < nblk) load_block(d, kr[d], vr[d]);
+    store_block(0, kr[0], vr[0]);
+    if (kFaD < nblk) load_block(kFaD, kr[0], vr[0]);
+  }
+  __syncthreads();
+  for (int b0 = 0; b0 < nblk; b0 += kFaD) {
+#pragma unroll
+    for (int u = 0; u < kFaD; ++u) {
+      const int b = b0 + u;
+      if (b < nblk) {
+        if (b + 1 < nblk) {
+          // block b + 1 (register set (u + 1) % kFaD) into the other slot: its
+          // last readers passed the previous barrier; then block b + 1 + kFaD
+          // into the freed registers
+          store_block((b + 1) & 1, kr[(u + 1) % kFaD], vr[(u + 1) % kFaD]);
+          if (b + 1 + kFaD < nblk) load_block(b + 1 + kFaD, kr[(u + 1) % kFaD], vr[(u + 1) % kFaD]);
+        }
+        compute(b, b & 1);
+        __syncthreads();
+      }
+    }
   }
   if (t < T) {
     const float inv = l > 0.f ? 1.f / l : 0.f;
