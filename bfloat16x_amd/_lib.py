@@ -93,6 +93,7 @@ TUNE_KEYS = {
     "gemm_ws_split": 5, "skinny_waves": 6, "skinny2_kq": 7, "skinny2_split": 8, "gemv_iters": 9, "gemv_g": 10,
     "gemv_long": 11, "gemv_xm_slots": 12, "gguf_long": 13, "gguf_iters": 14, "attn_split": 15,
     "gemm_ws_grouped": 16, "gemm_ws_resident": 17, "attn_mfma": 18,
+    "gemm_ws5_min_rows": 19,
 }
 
 _LIB = None

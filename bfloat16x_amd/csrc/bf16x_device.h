@@ -112,6 +112,70 @@ __device__ __forceinline__ uint32_t pk_ashr15(uint32_t a) {
 // (m & a) | (~m & b): v_bfi_b32
 __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) { return (m & a) | (~m & b); }
 
+// An atom's fields after the 16-bit-lane transposition (lane lo = elements
+// 0..15, lane hi = 16..31), ready for decode_pair.
+struct PairState {
+  uint32_t pm[7];   // mantissa words
+  uint32_t pd[3];   // code words
+  uint32_t E;       // emax of each half at bits 7..14 of its 16-bit lane
+  uint32_t s;       // sign word
+};
+
+__device__ __forceinline__ PairState prep_pairs(const Atom& t) {
+  PairState q;
+  q.pm[0] = lo_hi(t.m[0], t.m[3]);
+  q.pm[1] = alignbit(t.m[4], t.m[0], 16);
+  q.pm[2] = lo_hi(t.m[1], t.m[4]);
+  q.pm[3] = alignbit(t.m[5], t.m[1], 16);
+  q.pm[4] = lo_hi(t.m[2], t.m[5]);
+  q.pm[5] = alignbit(t.m[6], t.m[2], 16);
+  q.pm[6] = lo_hi(t.m[3], t.m[6]);
+  q.pd[0] = lo_hi(t.d[0], t.d[1]);
+  q.pd[1] = alignbit(t.d[2], t.d[0], 16);
+  q.pd[2] = lo_hi(t.d[1], t.d[2]);
+  const uint32_t e16 = t.e;
+  q.E = ((e16 & 0xFFu) << 7) | ((e16 & 0xFF00u) << 15);
+  q.s = t.s;
+  return q;
+}
+
+// Pair j (0..15, a compile-time constant after unrolling): bf16(elem j) |
+// bf16(elem j+16) << 16.
+template <bool ZERO7 = false>
+__device__ __forceinline__ uint32_t decode_pair(const PairState& q, int j) {
+  // mantissa field at lane bit 7j
+  const int mk = (7 * j) >> 4, mo = (7 * j) & 15;
+  uint32_t mraw;
+  if (mo <= 9) {
+    mraw = q.pm[mk] >> mo;
+  } else {
+    // field straddles two 16-bit chunks: splice byte 1 of chunk k with
+    // byte 0 of chunk k+1 in each lane, then the field sits at mo-8
+    mraw = perm(q.pm[mk + 1], q.pm[mk], 0x06030401u) >> (mo - 8);
+  }
+  // code field at lane bit 3j, moved to bits 7..9 of each lane
+  const int dk = (3 * j) >> 4, dof = (3 * j) & 15;
+  uint32_t dsh;
+  if (dof <= 13) {
+    dsh = (dof <= 7) ? (q.pd[dk] << (7 - dof)) : (q.pd[dk] >> (dof - 7));
+  } else {
+    dsh = perm(q.pd[dk + 1], q.pd[dk], 0x06030401u) << (15 - dof);
+  }
+  dsh &= 0x03800380u;
+  uint32_t ex;
+  if constexpr (ZERO7) {
+    const uint32_t t15 = (dsh << 5) + 0x10001000u;         // bit 15 of a lane set iff code == 7
+    ex = bfi(pk_ashr15(t15), 0u, pk_sub_wrap(q.E, dsh));    // (emax - d) << 7 mod 2^16, 0 for code 7
+  } else {
+    ex = pk_sub_sat(q.E, dsh);                             // (emax - d) << 7 per lane, clamped at 0
+  }
+  const uint32_t ssh = (j == 15) ? q.s : (q.s << (15 - j));
+  // v_bitop3 0xEA = (S0 & S1) | S2: mantissa bits into the exponent word,
+  // then the two sign bits (ex has zeros at both masks' positions)
+  uint32_t w = __builtin_amdgcn_bitop3_b32(mraw, 0x007F007Fu, ex, 0xEA);
+  return __builtin_amdgcn_bitop3_b32(ssh, 0x80008000u, w, 0xEA);
+}
+
 // Decode an atom into 16 packed pairs: out[j] = bf16(elem j) | bf16(elem j+16) << 16.
 // ZERO7 = false (packed dict): the 3-bit code is the exponent delta, code 7
 // saturating at emax-7; the exponent is clamped at 0 like the reference
@@ -123,57 +187,9 @@ __device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) { re
 // shift by 15 widens that bit to a lane mask which clears the exponent.
 template <bool ZERO7 = false>
 __device__ __forceinline__ void decode_pairs(const Atom& t, uint32_t out[16]) {
-  // 16-bit-lane transposition: lane lo = elements 0..15, lane hi = 16..31
-  uint32_t pm[7];
-  pm[0] = lo_hi(t.m[0], t.m[3]);
-  pm[1] = alignbit(t.m[4], t.m[0], 16);
-  pm[2] = lo_hi(t.m[1], t.m[4]);
-  pm[3] = alignbit(t.m[5], t.m[1], 16);
-  pm[4] = lo_hi(t.m[2], t.m[5]);
-  pm[5] = alignbit(t.m[6], t.m[2], 16);
-  pm[6] = lo_hi(t.m[3], t.m[6]);
-  uint32_t pd[3];
-  pd[0] = lo_hi(t.d[0], t.d[1]);
-  pd[1] = alignbit(t.d[2], t.d[0], 16);
-  pd[2] = lo_hi(t.d[1], t.d[2]);
-  // emax of each half at bits 7..14 of its 16-bit lane
-  const uint32_t e16 = t.e;
-  const uint32_t E = ((e16 & 0xFFu) << 7) | ((e16 & 0xFF00u) << 15);
+  const PairState q = prep_pairs(t);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
-    // mantissa field at lane bit 7j
-    const int mk = (7 * j) >> 4, mo = (7 * j) & 15;
-    uint32_t mraw;
-    if (mo <= 9) {
-      mraw = pm[mk] >> mo;
-    } else {
-      // field straddles two 16-bit chunks: splice byte 1 of chunk k with
-      // byte 0 of chunk k+1 in each lane, then the field sits at mo-8
-      mraw = perm(pm[mk + 1], pm[mk], 0x06030401u) >> (mo - 8);
-    }
-    // code field at lane bit 3j, moved to bits 7..9 of each lane
-    const int dk = (3 * j) >> 4, dof = (3 * j) & 15;
-    uint32_t dsh;
-    if (dof <= 13) {
-      dsh = (dof <= 7) ? (pd[dk] << (7 - dof)) : (pd[dk] >> (dof - 7));
-    } else {
-      dsh = perm(pd[dk + 1], pd[dk], 0x06030401u) << (15 - dof);
-    }
-    dsh &= 0x03800380u;
-    uint32_t ex;
-    if constexpr (ZERO7) {
-      const uint32_t t15 = (dsh << 5) + 0x10001000u;         // bit 15 of a lane set iff code == 7
-      ex = bfi(pk_ashr15(t15), 0u, pk_sub_wrap(E, dsh));      // (emax - d) << 7 mod 2^16, 0 for code 7
-    } else {
-      ex = pk_sub_sat(E, dsh);                               // (emax - d) << 7 per lane, clamped at 0
-    }
-    const uint32_t ssh = (j == 15) ? t.s : (t.s << (15 - j));
-    // v_bitop3 0xEA = (S0 & S1) | S2: mantissa bits into the exponent word,
-    // then the two sign bits (ex has zeros at both masks' positions)
-    uint32_t w = __builtin_amdgcn_bitop3_b32(mraw, 0x007F007Fu, ex, 0xEA);
-    w = __builtin_amdgcn_bitop3_b32(ssh, 0x80008000u, w, 0xEA);
-    out[j] = w;
-  }
+  for (int j = 0; j < 16; ++j) out[j] = decode_pair<ZERO7>(q, j);
 }
 
 // bf16 bits of a finite-or-not float, round to nearest even, NaN kept NaN.

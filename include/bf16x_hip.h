@@ -325,7 +325,8 @@ enum {
   BF16X_TUNE_GEMM_WS_GROUPED = 16, /* 0: the wave-specialised GEMM in one-step (64-column) tiles   */
   BF16X_TUNE_GEMM_WS_RESIDENT = 17,/* resident blocks the wave-specialised GEMM plans its rounds for */
   BF16X_TUNE_ATTN_MFMA = 18,       /* prefill attention: 0 the scalar kernel, 1 the MFMA kernel       */
-  BF16X_TUNE_COUNT = 19
+  BF16X_TUNE_GEMM_WS5_MIN_ROWS = 19,/* smallest M of the one-wave-per-SIMD GEMM (default 0: never) */
+  BF16X_TUNE_COUNT = 20
 };
 int bf16x_set_tuning(int32_t key, int64_t value);
 /* Current value of a key (-1 = automatic; also returned for an unknown key). */

@@ -102,6 +102,23 @@ def test_gemm_fused(bx, shape):
         check_tol(y3.float().cpu().numpy().reshape(-1, out_f), x3.double().numpy().reshape(-1, in_f) @ wdec.T)
 
 
+@pytest.mark.parametrize("shape", [(256, 4096), (1100, 1024)])
+def test_gemm_fused_ws5(bx, tune, shape):
+    """The one-wave-per-SIMD kernel on GGUF blocks, forced from one row: one
+    partial 512-row tile, one full and one partial."""
+    out_f, in_f = shape
+    print("gguf gemm ws5", shape, flush=True)
+    tune(gemm_ws5_min_rows=1)
+    w = gc.student_t_weights(out_f, in_f, seed=6)
+    blocks = bx.gguf.quantize_blocks(w)
+    wdec = gc.dequantize_blocks(blocks).astype(np.float64).reshape(out_f, in_f)
+    b = bx.gguf.device_blocks(blocks, DEV)
+    for M in (37, 700):
+        xm = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M + 1)).to(torch.bfloat16)
+        y = bx.gguf.gguf_gemm_fused(xm.to(DEV), b, out_f, in_f, out_dtype=torch.float32)
+        check_tol(y.cpu().numpy(), xm.double().numpy() @ wdec.T)
+
+
 def test_gemm_fused_refuses(bx):
     from bfloat16x_amd import Bf16xError
     w = gc.student_t_weights(8, 96, seed=1)
