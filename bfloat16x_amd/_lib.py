@@ -81,6 +81,12 @@ PROTOTYPES = {
                                            _P, _P, _P, _c_i64, _c_i64, _c_i32, _P, _P]),
     "bf16x_gemv_prenormed": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
                                             _P, _c_i64, _P, _P, _P, _c_i64, _c_i64, _c_i32, _c_i32, _P, _P]),
+    "bf16x_layer_front_sync_bytes": (_c_i64, []),
+    "bf16x_layer_front_decode": (ctypes.c_int, [_P, _P, ctypes.c_float, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P,
+                                                _c_i64, _P, _c_i64, _P, _P, _P, _c_i64, _c_i64, _c_i32, _P, _P, _P,
+                                                _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _P, _P, _P,
+                                                _P, _P, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
+                                                _P, _P, _P, _c_i64, _P, _P, _P, _c_i64, _P]),
     "bf16x_greedy": (ctypes.c_int, [_P, _c_i64, _P, _P, _P, _c_i64, _P]),
     # kernel-choice overrides (include/bf16x_hip.h)
     "bf16x_set_tuning": (ctypes.c_int, [_c_i32, _c_i64]),

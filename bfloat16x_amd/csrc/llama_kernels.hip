@@ -9,6 +9,7 @@
 // against ~340 MB of packed weights): they are written for few launches and
 // plain coalesced access, not for peak bandwidth.
 #include "bf16x_device.h"
+#include "gemv_pipe.h"
 #include "launch_common.h"
 #include "../../include/bf16x_llama.h"
 
@@ -886,12 +887,78 @@ constexpr int kDecHWaves = 16;
 constexpr int kDecHBlocks = 3;
 constexpr int kDecHMaxLen = 16 * kDecHWaves * kDecHBlocks;   // 768
 
-template <int G, int W = kDec1Waves, bool PH = false, int NB = 0>
-__global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __restrict__ qkv,
-                                                            const int32_t* __restrict__ pos,
-                                                            const float* __restrict__ cs, int H, int KV,
-                                                            int max_len, float scale, uint16_t* __restrict__ kc,
-                                                            uint16_t* __restrict__ vc, uint16_t* __restrict__ out) {
+// The layer launch (layer_front_kernel: the qkv GEMV, the decode attention and
+// optionally the o projection as one launch) orders its stages with
+// counters in device memory instead of launch boundaries.  A stage stores
+// what the next one reads with agent-coherent (write-through) stores; its
+// workgroups count themselves on counter (s, XCD of the workgroup) once
+// every wave's stores are complete (s_waitcnt vmcnt(0), then a barrier and
+// thread 0's device-scope atomic).  No release fence: its L2 write-back took
+// ~0.3 us per workgroup and they queue per XCD (7 us in the decode step).
+// Per-XCD counters because ~200 device-scope atomics on one address
+// serialise, ~5 us.  A waiting workgroup's thread 0 polls until the eight
+// counters of the stage before add up to its workgroup count; the data is
+// then read with agent-coherent loads (an acquire fence would invalidate the
+// XCD's L2, ~3 us).  The counters are never reset by
+// the launch that uses them: each launch zeroes those of the launch before
+// it (`clear`), which stream order has finished.  The waits are bounded:
+// past kSyncSpinLimit polls the workgroup sets `err` and goes on.
+constexpr int kSyncXcds = 8;
+constexpr int kSyncStride = 64;                 // words: one 256-byte line per counter
+constexpr int kSyncStages = 2;                  // counted stages: the qkv GEMV, the attention
+constexpr int kSyncErrWord = kSyncStages * kSyncXcds * kSyncStride;
+constexpr uint32_t kSyncSpinLimit = 1u << 19;   // a few tenths of a second of polls
+constexpr int kWaitVmcnt0 = 0x0F70;             // s_waitcnt vmcnt(0) expcnt(7) lgkmcnt(15) (gfx9 encoding)
+
+__device__ __forceinline__ uint32_t* sync_counter(uint32_t* sync, int stage, int xcd) {
+  return sync + (stage * kSyncXcds + xcd) * kSyncStride;
+}
+
+// Thread 0 waits until the counters of `stage` reach `target`; then the
+// barrier releases the workgroup.  Called by every thread.
+__device__ __forceinline__ void sync_wait(uint32_t* sync, int stage, uint32_t target) {
+  if (threadIdx.x == 0) {
+    auto counted = [&]() {
+      uint32_t t = 0;
+#pragma unroll
+      for (int x = 0; x < kSyncXcds; ++x)
+        t += __hip_atomic_load(sync_counter(sync, stage, x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return t;
+    };
+    uint32_t spins = 0;
+    while (counted() < target) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins == kSyncSpinLimit) {
+        __hip_atomic_store(sync + kSyncErrWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// Every wave's stores are complete, then thread 0 counts the workgroup on
+// (stage, xcd).  Called by every thread.
+__device__ __forceinline__ void sync_count(uint32_t* sync, int stage, int xcd) {
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  __syncthreads();
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(sync_counter(sync, stage, xcd), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// WAIT: the attention workgroups of the layer launch wait for the qkv GEMV
+// (stage 0, `target` workgroups) before reading qkv, and count themselves on
+// stage 1 when their output is stored.
+struct AttnSync {
+  uint32_t* sync;
+  uint32_t target;
+};
+
+template <int G, int W, bool PH, int NB, bool WAIT = false>
+__device__ __forceinline__ void attn_decode1_body(const uint16_t* __restrict__ qkv, const int32_t* __restrict__ pos,
+                                                  const float* __restrict__ cs, int H, int KV, int max_len,
+                                                  float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                                  uint16_t* __restrict__ out, int blk, int tid, AttnSync sync) {
   __shared__ uint32_t qs2[G][64];          // rotated q as bf16 pairs (dims 2i, 2i+1)
   __shared__ uint32_t kp2[64];             // the new key, likewise
   __shared__ float vp[128];
@@ -905,10 +972,10 @@ __global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __
   // of a KV head are KV blocks apart: with KV = 8 they run on one XCD
   // (blocks go round-robin over the 8 XCDs) and share its L2 for the K / V rows
   const int gq = H / KV;
-  const int g = PH ? (int)blockIdx.x % KV : (int)blockIdx.x;
-  const int hq0 = PH ? g * gq + (int)blockIdx.x / KV : g * G;
-  const bool writer = !PH || (int)blockIdx.x < KV;         // appends the new K / V row
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int g = PH ? blk % KV : blk;
+  const int hq0 = PH ? g * gq + blk / KV : g * G;
+  const bool writer = !PH || blk < KV;                     // appends the new K / V row
+  const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = lane >> 2, q4 = lane & 3;
   // NB > 0: the entry loads are issued before the position is read,
@@ -956,6 +1023,7 @@ __global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __
     load_k(1, kR[1]);
     load_v(1, vR[1]);
   }
+  if constexpr (WAIT) sync_wait(sync.sync, 0, sync.target);
   // rotary embedding of the q heads and the new key, KV append
   {
     const int pc = pp < 0 ? 0 : (pp >= max_len ? max_len - 1 : pp);
@@ -963,7 +1031,17 @@ __global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __
       const float c = cs[((int64_t)pc * 64 + lane) * 2], sn = cs[((int64_t)pc * 64 + lane) * 2 + 1];
       const int head = hh < G ? hq0 + hh : (hh == G ? H + g : H + KV + g);
       const uint16_t* src = qkv + (int64_t)head * 128;
-      const uint16_t a16 = src[lane], b16 = src[lane + 64];
+      uint16_t a16, b16;
+      if constexpr (WAIT) {
+        // written by other workgroups of this launch (other XCDs): loads
+        // that are coherent at agent scope, issued after the count was seen
+        const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)src, (short)0, 256, 0x00020000);
+        a16 = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rq, 2 * lane, 0, kCoherentLoad);
+        b16 = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rq, 2 * lane + 128, 0, kCoherentLoad);
+      } else {
+        a16 = src[lane];
+        b16 = src[lane + 64];
+      }
       if (hh <= G) {
         const float a = bfv(a16), b = bfv(b16);
         const uint32_t ra = f32_to_bf16_rne(a * c - b * sn), rb = f32_to_bf16_rne(b * c + a * sn);
@@ -1130,8 +1208,24 @@ __global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __
       L = fmaf(wl[k][h], f, L);
       o = fmaf(wacc[k][h][d], f, o);
     }
-    out[(int64_t)(hq0 + h) * 128 + d] = (uint16_t)f32_to_bf16_rne(L > 0.f ? o / L : 0.f);
+    const uint16_t ob = (uint16_t)f32_to_bf16_rne(L > 0.f ? o / L : 0.f);
+    if constexpr (WAIT)   // read by the o projection's workgroups of this launch
+      __builtin_amdgcn_raw_buffer_store_b16(ob, __builtin_amdgcn_make_buffer_rsrc(out, (short)0, H * 256, 0x00020000),
+                                            (hq0 + h) * 256 + 2 * d, 0, kCoherentLoad);
+    else
+      out[(int64_t)(hq0 + h) * 128 + d] = ob;
   }
+  if constexpr (WAIT) sync_count(sync.sync, 1, blk & (kSyncXcds - 1));
+}
+
+template <int G, int W = kDec1Waves, bool PH = false, int NB = 0>
+__global__ __launch_bounds__(64 * W) void attn_decode1_kernel(const uint16_t* __restrict__ qkv,
+                                                            const int32_t* __restrict__ pos,
+                                                            const float* __restrict__ cs, int H, int KV,
+                                                            int max_len, float scale, uint16_t* __restrict__ kc,
+                                                            uint16_t* __restrict__ vc, uint16_t* __restrict__ out) {
+  attn_decode1_body<G, W, PH, NB>(qkv, pos, cs, H, KV, max_len, scale, kc, vc, out, (int)blockIdx.x,
+                                  (int)threadIdx.x, AttnSync{nullptr, 0u});
 }
 
 
@@ -1206,6 +1300,211 @@ extern "C" int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, c
     default: BF16X_DEC(8); break;
   }
 #undef BF16X_DEC
+  return launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// The front of a decoder layer for one decode token in one launch: the qkv
+// projection (with its RMSNorm from the residual GEMV's slots), the decode
+// attention and, optionally, the o projection with the residual add.
+// Hardware workgroups of 1024 threads, in dispatch order:
+//  - 0 .. H-1: the per-query-head attention workgroups of attn_decode1_kernel
+//    (16 waves, the 768-row variant); they request their K / V rows and the
+//    position at entry, i.e. while the GEMV streams its weights;
+//  - nq qkv GEMV workgroups, each four 4-wave workgroups of gemv_pipe_body
+//    (XM = 2, the rows of bf16x_gemv_prenormed); they wait for nothing;
+//  - no o GEMV workgroups (four of gemv_pipe_body with the residual epilogue
+//    each, the rows and slots of bf16x_gemv_residual); they request their
+//    first rows, then wait for the attention.
+// Stages are ordered by the counters of `sync` (see sync_wait).  No workgroup
+// waits for a later one in dispatch order, and the waiting attention
+// workgroups hold at most half of the CUs, so every wait ends.  Outputs are
+// bit-identical to bf16x_gemv_prenormed, bf16x_attention_decode and
+// bf16x_gemv_residual in sequence.
+constexpr int kQaSubs = 4;                      // GEMV workgroups per hardware workgroup
+constexpr int kQaThreads = 64 * kDecHWaves;     // 1024
+static_assert(kQaThreads == 256 * kQaSubs, "four 256-thread GEMV workgroups per attention-sized workgroup");
+// x staging of one GEMV workgroup (NS = 2): 8 KB.  The four GEMV workgroups
+// of a hardware workgroup stage the same x (it depends only on the thread's
+// slot), so they share one copy: each thread's store is made by the
+// matching thread of every workgroup with the same value, before the barrier
+// that every reader waits at.
+constexpr int kQaSubLdsWords = 2 * 64 * 4 * 4;
+
+// The o projection's wait: the attention workgroups (stage 1) are done.
+struct OWait {
+  static constexpr bool active = true;
+  uint32_t* sync;
+  uint32_t target;
+  __device__ void operator()() const { sync_wait(sync, 1, target); }
+};
+
+// Inverse of xcd_row_block(., nb): the block index of a standalone launch of
+// nb workgroups whose row block is q (its slot of bf16x_gemv_residual).
+__device__ __forceinline__ int xcd_block_of_row_block(int q, int nb) {
+  if (nb < 8) return q;
+  const int per = nb / 8, extra = nb - per * 8;
+  int x = 0;
+#pragma unroll
+  for (int t = 1; t < 8; ++t) x += q >= t * per + min(t, extra) ? 1 : 0;
+  return (q - (x * per + min(x, extra))) * 8 + x;
+}
+
+struct OStage {
+  const uint16_t* res_in;
+  uint16_t* res_out;
+  float* slots;
+  const uint32_t* sign;
+  const uint32_t* mant;
+  const uint32_t* delta;
+  const uint16_t* emax2;
+  const uint32_t* tile_off;
+  const uint32_t* tile_ent;
+  const uint8_t* tile_sat;
+  int64_t out_f;
+  uint16_t* y;
+  int nblocks;         // workgroups of the standalone residual launch (its slots)
+  int iters;           // row groups of 4 per workgroup there
+};
+
+template <bool EXACT, bool FULL>
+__global__ __launch_bounds__(kQaThreads) void layer_front_kernel(
+    const uint16_t* h, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
+    const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2, const uint32_t* __restrict__ tile_off,
+    const uint32_t* __restrict__ tile_ent, const uint8_t* __restrict__ tile_sat, int64_t out_f, int64_t in_f,
+    int iters, NormArgs na, uint16_t* qkv, const int32_t* __restrict__ pos, const float* __restrict__ cs, int H,
+    int KV, int max_len, float scale, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, uint16_t* attn_out,
+    int nq, OStage os, uint32_t* sync, uint32_t* clear) {
+  extern __shared__ uint32_t qa_lds[];
+  const int b = (int)blockIdx.x;
+  if (b == 0 && threadIdx.x == 0 && clear != nullptr) {
+    // the launch before this one (finished: stream order) used `clear`
+#pragma unroll
+    for (int c = 0; c < kSyncStages * kSyncXcds; ++c) clear[c * kSyncStride] = 0u;
+  }
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);   // kept in a scalar register
+  const int sub = wave >> 2;
+  if (b < H) {
+    attn_decode1_body<1, kDecHWaves, true, kDecHBlocks, true>(qkv, pos, cs, H, KV, max_len, scale, kc, vc,
+                                                              attn_out, b, (int)threadIdx.x,
+                                                              AttnSync{sync, (uint32_t)nq});
+    return;
+  }
+  // H % 8 == 0 and nq % 8 == 0 (checked by the launcher): GEMV workgroup gb
+  // of either stage runs on XCD gb % 8
+  if (b < H + nq) {
+    const int gb = b - H;
+    const int lb = kQaSubs * xcd_row_block(gb, nq) + sub;
+    gemv_pipe_body<2, 1, BF16X_BF16, EXACT, FULL, 0, 2, 0, kQaSubs, NoPreWait, true>(
+        h, sign, mant, delta, emax2, tile_off, tile_ent, tile_sat, out_f, in_f, iters, qkv, na,
+        ResArgs{nullptr, nullptr, nullptr}, (int)threadIdx.x & 255, sub, kQaSubs * gb + sub, lb, qa_lds);
+    sync_count(sync, 0, gb & (kSyncXcds - 1));
+    return;
+  }
+  const int ob = b - H - nq, nob = (int)gridDim.x - H - nq;
+  const int lb = kQaSubs * xcd_row_block(ob, nob) + sub;       // row groups lb iters ..
+  gemv_pipe_body<2, 1, BF16X_BF16, EXACT, FULL, 0, 0, 1, kQaSubs, OWait>(
+      attn_out, os.sign, os.mant, os.delta, os.emax2, os.tile_off, os.tile_ent, os.tile_sat, os.out_f,
+      (int64_t)H * 128, os.iters, os.y, NormArgs{nullptr, nullptr, nullptr, 0.f, nullptr, 0},
+      ResArgs{os.res_in, os.res_out, os.slots}, (int)threadIdx.x & 255, sub,
+      lb < os.nblocks ? xcd_block_of_row_block(lb, os.nblocks) : -1, lb, qa_lds, OWait{sync, (uint32_t)H});
+}
+
+extern "C" int64_t bf16x_layer_front_sync_bytes(void) { return 4 * (kSyncErrWord + 4); }
+
+extern "C" int bf16x_layer_front_decode(
+    const void* h, const uint16_t* norm_weight, float eps, const float* slots, int64_t n_slots, const int32_t* sign,
+    int64_t n_sign, const int32_t* mant, int64_t n_mant, const int32_t* delta, int64_t n_delta, const uint8_t* emax,
+    int64_t n_emax, const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
+    int64_t in_f, int32_t mode, uint16_t* qkv, const int32_t* pos, const float* cos_sin, int64_t n_heads,
+    int64_t n_kv_heads, int64_t head_dim, int64_t max_len, float scale, uint16_t* k_cache, uint16_t* v_cache,
+    uint16_t* attn_out, const uint16_t* o_residual_in, uint16_t* o_residual_out, float* o_slots, int64_t o_n_slots,
+    const int32_t* o_sign, int64_t o_n_sign, const int32_t* o_mant, int64_t o_n_mant, const int32_t* o_delta,
+    int64_t o_n_delta, const uint8_t* o_emax, int64_t o_n_emax, const uint32_t* o_tile_off,
+    const uint32_t* o_tile_ent, const uint8_t* o_tile_sat, int64_t o_out_f, uint16_t* o_y, void* sync,
+    void* sync_clear, int64_t sync_bytes, bf16x_stream_t stream) {
+  if (!h || !norm_weight || !slots || !sign || !mant || !delta || !emax || !qkv || !pos || !cos_sin || !k_cache ||
+      !v_cache || !sync || !attn_out)
+    return BF16X_EARG;
+  if (mode != BF16X_EXACT && mode != BF16X_SATURATED) return BF16X_EARG;
+  const bool ex = mode == BF16X_EXACT;
+  if (ex && (!tile_off || !tile_ent || !tile_sat)) return BF16X_EARG;
+  int rc = check_dict(out_f, in_f, 16, n_sign, n_mant, n_delta, n_emax);
+  if (rc) return rc;
+  if (sync_bytes < bf16x_layer_front_sync_bytes()) return BF16X_ECAPACITY;
+  if (sync_clear == sync) return BF16X_EARG;
+  if (n_slots <= 0) return BF16X_EARG;
+  if (n_slots > 64 * kMaxSlotsPerLane) return BF16X_ECAPACITY;
+  // the attention side: the per-query-head kernel's shapes; n_heads <= 128:
+  // the waiting attention workgroups hold at most half of the CUs
+  if (head_dim != 128 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads % 8 != 0 ||
+      n_heads > 128 || max_len <= kDec1MaxLen || max_len > kDecHMaxLen)
+    return BF16X_ESHAPE;
+  // the GEMV side: 64 < in_f / 32 <= 128 (two 64-atom steps per wave, one
+  // wave per row), out_f = the qkv rows of the attention
+  if (out_f != (n_heads + 2 * n_kv_heads) * 128) return BF16X_ESHAPE;
+  const int64_t P = in_f >> 5;
+  if (in_f % 32 != 0 || P <= 64 || P > 128 || (out_f + 1) * P * 28 >= (int64_t)0xFFFFFFFF) return BF16X_ESHAPE;
+  if (!aligned4(h) || !aligned4(norm_weight) || !aligned4(slots) || !aligned4(sign) || !aligned4(mant) ||
+      !aligned4(delta) || !aligned2(emax) || !aligned16(k_cache) || !aligned4(v_cache) || !aligned4(cos_sin) ||
+      !aligned4(qkv) || !aligned4(attn_out) || !aligned16(sync) || !aligned16(sync_clear))
+    return BF16X_EARG;
+  // the o stage (optional: o_sign NULL): a packed dict [o_out_f, n_heads * 128]
+  // in the same mode and with in_f's step count, residual buffers of o_out_f
+  const bool has_o = o_sign != nullptr;
+  OStage os{};
+  int64_t no = 0;
+  int o_iters = 1;
+  if (has_o) {
+    if (!o_residual_in || !o_residual_out || !o_slots || !o_mant || !o_delta || !o_emax || !o_y) return BF16X_EARG;
+    if (ex && (!o_tile_off || !o_tile_ent || !o_tile_sat)) return BF16X_EARG;
+    if (n_heads * 128 != in_f) return BF16X_ESHAPE;
+    rc = check_dict(o_out_f, in_f, 16, o_n_sign, o_n_mant, o_n_delta, o_n_emax);
+    if (rc) return rc;
+    if ((o_out_f + 1) * P * 28 >= (int64_t)0xFFFFFFFF) return BF16X_ESHAPE;
+    // o_slots may be `slots`: the o stage writes them after every qkv
+    // workgroup has read its sums (it waits for the attention, which waits
+    // for the qkv GEMV)
+    if ((const void*)o_residual_out == (const void*)o_residual_in || o_residual_out == o_y ||
+        (const void*)o_residual_out == h)
+      return BF16X_EARG;
+    // the o workgroups take the row groups of the standalone residual
+    // launch's workgroups (1 or 2 groups of 4 rows each) and write their
+    // slots (through the XCD mapping)
+    const int64_t nb_res = bf16x_gemv_residual_slots(o_out_f, in_f);
+    const int64_t groups_o = (o_out_f + 3) / 4;
+    if (nb_res <= 0) return BF16X_ESHAPE;
+    o_iters = (int)((groups_o + nb_res - 1) / nb_res);
+    if (o_iters > 2 || (groups_o + o_iters - 1) / o_iters != nb_res) return BF16X_ESHAPE;
+    if (o_n_slots < nb_res) return BF16X_ECAPACITY;
+    if (!aligned4(o_sign) || !aligned4(o_mant) || !aligned4(o_delta) || !aligned2(o_emax) ||
+        !aligned2(o_residual_in) || !aligned2(o_residual_out) || !aligned4(o_slots) || !aligned2(o_y))
+      return BF16X_EARG;
+    no = (nb_res + kQaSubs - 1) / kQaSubs;
+    os = OStage{o_residual_in, o_residual_out, o_slots, (const uint32_t*)o_sign, (const uint32_t*)o_mant,
+                (const uint32_t*)o_delta, (const uint16_t*)o_emax, ex ? o_tile_off : nullptr,
+                ex ? o_tile_ent : nullptr, ex ? o_tile_sat : nullptr, o_out_f, o_y, (int)nb_res, o_iters};
+  }
+  const bool full = P == 128;
+  // GEMV rows per 4-wave workgroup as the standalone launch (bf16x_gemv_prenormed)
+  const int64_t groups = (out_f + 3) / 4;
+  const int iters = groups >= 1024 ? 2 : 1;
+  const int64_t vblocks = (groups + iters - 1) / iters;
+  const int64_t nq = 8 * ((vblocks + 8 * kQaSubs - 1) / (8 * kQaSubs));   // a multiple of 8 (XCD mapping)
+  if (nq + n_heads + no > INT32_MAX) return BF16X_ESHAPE;
+  const NormArgs na{nullptr, norm_weight, nullptr, eps, slots, (int)n_slots};
+  const size_t lds = (size_t)kQaSubLdsWords * 4;
+  const uint32_t *to = ex ? tile_off : nullptr, *te = ex ? tile_ent : nullptr;
+  const uint8_t* ts = ex ? tile_sat : nullptr;
+#define BF16X_LF(EX_, FULL_)                                                                                      \
+  hipLaunchKernelGGL((layer_front_kernel<EX_, FULL_>), dim3((unsigned)(n_heads + nq + no)), dim3(kQaThreads), lds, \
+                     (hipStream_t)stream, (const uint16_t*)h, (const uint32_t*)sign, (const uint32_t*)mant,         \
+                     (const uint32_t*)delta, (const uint16_t*)emax, to, te, ts, out_f, in_f, iters, na, qkv, pos,  \
+                     cos_sin, (int)n_heads, (int)n_kv_heads, (int)max_len, scale, k_cache, v_cache, attn_out,     \
+                     (int)nq, os, (uint32_t*)sync, (uint32_t*)sync_clear)
+  if (ex) { if (full) BF16X_LF(true, true); else BF16X_LF(true, false); }
+  else { if (full) BF16X_LF(false, true); else BF16X_LF(false, false); }
+#undef BF16X_LF
   return launch_status();
 }
 

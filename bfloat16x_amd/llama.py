@@ -46,7 +46,8 @@ from torch import nn
 from . import _lib, ops
 
 __all__ = ["LlamaConfig", "LlamaStack", "LlamaRunner", "rope_table", "rmsnorm", "rope_kv", "attention", "pairs8_rows",
-           "attention_decode", "attention_decode_supported", "attention_decode_workspace", "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
+           "attention_decode", "attention_decode_supported", "attention_decode_workspace", "layer_front_decode",
+           "layer_front_supported", "layer_front_sync", "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
 
 NORM_ADD, NORM_STORE = 1, 2
 HEAD_DIM = 128
@@ -202,6 +203,72 @@ def attention_decode(qkv, pos, cos_sin, n_heads, n_kv_heads, k_cache, v_cache, o
     _lib.check(st, "bf16x_attention_decode")
 
 
+def layer_front_supported(n_heads, n_kv_heads, max_len, out_f, in_f) -> bool:
+    """Shapes bf16x_layer_front_decode takes (the per-query-head attention,
+    one wave per qkv row with two 64-atom steps)."""
+    return (n_heads % 8 == 0 and n_heads <= 128 and n_heads % n_kv_heads == 0 and 256 < max_len <= 768
+            and in_f % 32 == 0 and 2048 < in_f <= 4096 and out_f == (n_heads + 2 * n_kv_heads) * HEAD_DIM)
+
+
+def layer_front_sync(device, n: int = 1) -> torch.Tensor:
+    """n zeroed counter buffers of layer_front_decode, one per row (word 1024
+    of a row: the timeout flag)."""
+    words = int(_lib.lib().bf16x_layer_front_sync_bytes()) // 4
+    words = -(-words // 4) * 4                                   # rows 16-byte aligned
+    return torch.zeros(n, words, dtype=torch.int32, device=device)
+
+
+def _dict_args(mod):
+    plan = mod._plan
+    return (mod._sign.data_ptr(), mod._sign.numel(), mod._mant.data_ptr(), mod._mant.numel(), mod._delta.data_ptr(),
+            mod._delta.numel(), mod._emax.data_ptr(), mod._emax.numel(), _lib.ptr(plan.tile_off) if plan else None,
+            _lib.ptr(plan.tile_ent) if plan else None, _lib.ptr(plan.tile_sat) if plan else None)
+
+
+def layer_front_decode(h, norm_weight, eps, slots, n_slots, mod, pos, cos_sin, n_heads, n_kv_heads, k_cache,
+                       v_cache, qkv_out, attn_out, sync, sync_clear=None, o=None, scale=None):
+    """bf16x_gemv_prenormed(h, ...) of the qkv module `mod` into qkv_out, then
+    attention_decode into attn_out and, with o = (o_mod, residual_in,
+    residual_out, o_slots, o_y), bf16x_gemv_residual(attn_out, ...) of the o
+    module, in one launch (bf16x_layer_front_decode).  `sync` must be zero;
+    the launch zeroes `sync_clear` (the previous launch's buffer)."""
+    for t, nm in ((h, "h"), (norm_weight, "norm_weight"), (qkv_out, "qkv_out"), (k_cache, "k_cache"),
+                  (v_cache, "v_cache"), (attn_out, "attn_out")):
+        _bf16_dev(t, nm)
+    _check_pos(pos)
+    out_f, in_f = mod.out_features, mod.in_features
+    max_len = k_cache.numel() // (n_kv_heads * HEAD_DIM)
+    _need(layer_front_supported(n_heads, n_kv_heads, max_len, out_f, in_f), "shape not supported")
+    _need(h.numel() == in_f and norm_weight.numel() == in_f, "h / norm_weight must hold in_f values")
+    _need(qkv_out.numel() == out_f and attn_out.numel() >= n_heads * HEAD_DIM, "qkv_out / attn_out size")
+    _need(k_cache.numel() == max_len * n_kv_heads * HEAD_DIM and v_cache.numel() == k_cache.numel(), "cache shape")
+    _need(cos_sin.is_cuda and cos_sin.dtype == torch.float32 and cos_sin.numel() == max_len * HEAD_DIM,
+          "cos_sin must be fp32 [max_len, 64, 2] on the GPU")
+    _need(slots.is_cuda and slots.dtype == torch.float32 and slots.numel() >= n_slots, "slots")
+    nbytes = int(_lib.lib().bf16x_layer_front_sync_bytes())
+    for t in (sync,) + ((sync_clear,) if sync_clear is not None else ()):
+        _need(t.is_cuda and t.is_contiguous() and t.numel() * t.element_size() >= nbytes, "sync buffers")
+    o_args = (None,) * 3 + (0,) + (None, 0) * 4 + (None,) * 3 + (0, None)
+    if o is not None:
+        o_mod, res_in, res_out, o_slots, o_y = o
+        _need(o_mod.in_features == in_f, "o projection must take in_f inputs")
+        for t, nm in ((res_in, "residual_in"), (res_out, "residual_out"), (o_y, "o_y")):
+            _bf16_dev(t, nm)
+            _need(t.numel() == o_mod.out_features, f"{nm} must hold o.out_features values")
+        _need(o_slots.is_cuda and o_slots.dtype == torch.float32, "o_slots must be fp32 on the GPU")
+        o_args = (res_in.data_ptr(), res_out.data_ptr(), o_slots.data_ptr(), o_slots.numel()) + \
+            _dict_args(o_mod) + (o_mod.out_features, o_y.data_ptr())
+    plan = mod._plan
+    scale = 1.0 / math.sqrt(HEAD_DIM) if scale is None else scale
+    st = _lib.lib().bf16x_layer_front_decode(
+        h.data_ptr(), norm_weight.data_ptr(), float(eps), slots.data_ptr(), int(n_slots), *_dict_args(mod), out_f,
+        in_f, _lib.EXACT if plan is not None else _lib.SATURATED, qkv_out.data_ptr(), pos.data_ptr(),
+        cos_sin.data_ptr(), n_heads, n_kv_heads, HEAD_DIM, max_len, float(scale), k_cache.data_ptr(),
+        v_cache.data_ptr(), attn_out.data_ptr(), *o_args, sync.data_ptr(),
+        sync_clear.data_ptr() if sync_clear is not None else None, nbytes, _stream(h))
+    _lib.check(st, "bf16x_layer_front_decode")
+
+
 def pairs8_rows(ffn: int) -> torch.Tensor:
     """Natural row of each row of a PAIRS8 gate_up weight: groups of 8 rows
     [gate 4b .. 4b+3, up 4b .. 4b+3] from the natural [gate; up] order."""
@@ -329,7 +396,7 @@ class LlamaRunner:
     history and advances the position."""
 
     def __init__(self, model: LlamaStack, max_len: int, max_new: int, max_prompt: int | None = None,
-                 norm_in_gemv: bool = False, residual_norm: bool = True):
+                 norm_in_gemv: bool = False, residual_norm: bool = True, layer_front: bool = True):
         cfg = model.cfg
         self.model, self.cfg = model, cfg
         dev = model.device
@@ -379,6 +446,18 @@ class LlamaRunner:
             self.n_slots_down = ops.gemv_residual_slots(lay0.down.out_features, lay0.down.in_features)
             self.slots = torch.zeros(max(self.n_slots_o, self.n_slots_down), dtype=torch.float32, device=dev)
             self.proj_out = torch.empty(cfg.hidden, **bf)     # o / down outputs (only h is used)
+        # layer_front (default, residual_norm stacks of 3 layers or more): layers after the first run the qkv
+        # GEMV, the decode attention and the o GEMV as one launch (bf16x_layer_front_decode).  Launch i (layer
+        # i + 1) uses counter buffer c(i) and zeroes its predecessor's, so consecutive launches, cyclically over
+        # the step (the graph repeats it), must differ: c = 0, 1, 0, 1, ..., and 2 for the last launch
+        lay0 = model.layers[0]
+        self.front = bool(layer_front) and self.res_norm and cfg.n_layers >= 3 and layer_front_supported(
+            cfg.n_heads, cfg.n_kv_heads, self.max_len, lay0.qkv.out_features, lay0.qkv.in_features) and \
+            lay0.o.in_features == lay0.qkv.in_features
+        if self.front:
+            self.front_sync = layer_front_sync(dev, 3)
+            n_f = cfg.n_layers - 1
+            self.front_buf = [(k % 2) if k < n_f - 1 else 2 for k in range(n_f)]
         self._prompt_len = 0
 
     def _decode_fused(self, pos: torch.Tensor, ids: torch.Tensor):
@@ -417,7 +496,9 @@ class LlamaRunner:
         from the previous down GEMV's sums of squares; the first layer takes
         the embedding's RMSNorm), attention, o GEMV (+ residual, sums of
         squares), gate_up GEMV (normalised input, SwiGLU), down GEMV (+
-        residual, sums of squares).  Returns h after the last layer."""
+        residual, sums of squares); with layer_front the qkv GEMV, the
+        attention and the o GEMV of every layer after the first are one
+        launch.  Returns h after the last layer."""
         cfg, m = self.cfg, self.model
         H, KV = cfg.n_heads, cfg.n_kv_heads
         R = (self.res_a, self.res_b)
@@ -425,15 +506,23 @@ class LlamaRunner:
         rmsnorm(m.embed, m.layers[0].attn_norm, self.normed, R[0], row_idx=ids, flags=NORM_STORE, eps=cfg.eps)
         for i, lay in enumerate(m.layers):
             q, o, g, d = lay.qkv, lay.o, lay.gate_up, lay.down
-            if i == 0:
-                qkv = q(self.normed[0])
+            if self.front and i > 0:
+                fb = self.front_buf              # launch i - 1: its buffer, then its predecessor's (cyclic)
+                layer_front_decode(R[cur], lay.attn_norm, cfg.eps, self.slots, self.n_slots_down, q, pos,
+                                   self.cos_sin, H, KV, self.k_cache[i], self.v_cache[i], self.qkv_buf, self.attn[0],
+                                   self.front_sync[fb[i - 1]], self.front_sync[fb[i - 2]],
+                                   o=(o, R[cur], R[1 - cur], self.slots, self.proj_out))
             else:
-                qkv = ops.bf16x_gemv_prenormed(R[cur], lay.attn_norm, cfg.eps, self.slots, self.n_slots_down, q._sign,
-                                               q._mant, q._delta, q._emax, q.out_features, q.in_features,
-                                               plan=q._plan, out=self.qkv_buf)
-            attention_decode(qkv, pos, self.cos_sin, H, KV, self.k_cache[i], self.v_cache[i], self.attn, self.dec_ws)
-            ops.bf16x_gemv_residual(self.attn[0], R[cur], R[1 - cur], self.slots, o._sign, o._mant, o._delta, o._emax,
-                                    o.out_features, o.in_features, plan=o._plan, out=self.proj_out)
+                if i == 0:
+                    qkv = q(self.normed[0])
+                else:
+                    qkv = ops.bf16x_gemv_prenormed(R[cur], lay.attn_norm, cfg.eps, self.slots, self.n_slots_down,
+                                                   q._sign, q._mant, q._delta, q._emax, q.out_features, q.in_features,
+                                                   plan=q._plan, out=self.qkv_buf)
+                attention_decode(qkv, pos, self.cos_sin, H, KV, self.k_cache[i], self.v_cache[i], self.attn,
+                                 self.dec_ws)
+                ops.bf16x_gemv_residual(self.attn[0], R[cur], R[1 - cur], self.slots, o._sign, o._mant, o._delta,
+                                        o._emax, o.out_features, o.in_features, plan=o._plan, out=self.proj_out)
             cur = 1 - cur
             ops.bf16x_gemv_prenormed(R[cur], lay.mlp_norm, cfg.eps, self.slots, self.n_slots_o, g._sign, g._mant,
                                      g._delta, g._emax, g.out_features, g.in_features, plan=g._plan, swiglu=True,

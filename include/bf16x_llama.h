@@ -149,6 +149,43 @@ int bf16x_gemv_prenormed(const void* h, const uint16_t* norm_weight, float eps, 
                          const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat, int64_t out_f,
                          int64_t in_f, int32_t mode, int32_t epilogue, uint16_t* y, bf16x_stream_t stream);
 
+/* The front of a decoder layer for one decode token in one launch: the qkv
+ * projection bf16x_gemv_prenormed (epilogue 0) into qkv, the decode attention
+ * bf16x_attention_decode (tokens = 1) into attn_out, and, when o_sign is not
+ * NULL, the o projection with the residual add bf16x_gemv_residual(attn_out,
+ * o_residual_in, o_residual_out, o_slots, o_*) into o_y; results are
+ * bit-identical to those launches in sequence.  The stages are ordered by
+ * device counters in `sync` instead of launch boundaries: the attention
+ * workgroups request their K / V cache rows while the qkv projection streams
+ * its weights, and the o projection's workgroups request their first rows
+ * while the attention runs.  Shapes: head_dim 128, n_heads % 8 == 0,
+ * n_heads <= 128, 256 < max_len <= 768 (the one-workgroup-per-query-head
+ * attention), out_f = (n_heads + 2 n_kv_heads) * 128, 2048 < in_f <= 4096,
+ * in_f % 32 == 0; the o stage: o dict [o_out_f, in_f] with in_f = n_heads *
+ * 128, in the same mode, a shape bf16x_gemv_residual runs with one or two
+ * groups of 4 rows per workgroup (it writes the bf16x_gemv_residual_slots(
+ * o_out_f, in_f) slots of that launch).  `sync`: bf16x_layer_front_sync_bytes()
+ * bytes, 16-byte aligned, all zero when the launch starts; the launch zeroes
+ * `sync_clear` (NULL: none; never `sync`), which must be the buffer of a
+ * launch that stream order has finished.  Consecutive launches therefore use
+ * different buffers, each clearing its predecessor's.  Word 1024 of `sync`
+ * becomes 1 if a wait ran out (a few tenths of a second; the outputs are then
+ * not valid); the caller clears it. */
+int64_t bf16x_layer_front_sync_bytes(void);
+int bf16x_layer_front_decode(const void* h, const uint16_t* norm_weight, float eps, const float* slots, int64_t n_slots,
+                             const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                             const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                             const uint32_t* tile_off, const uint32_t* tile_ent, const uint8_t* tile_sat,
+                             int64_t out_f, int64_t in_f, int32_t mode, uint16_t* qkv, const int32_t* pos,
+                             const float* cos_sin, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                             int64_t max_len, float scale, uint16_t* k_cache, uint16_t* v_cache, uint16_t* attn_out,
+                             const uint16_t* o_residual_in, uint16_t* o_residual_out, float* o_slots,
+                             int64_t o_n_slots, const int32_t* o_sign, int64_t o_n_sign, const int32_t* o_mant,
+                             int64_t o_n_mant, const int32_t* o_delta, int64_t o_n_delta, const uint8_t* o_emax,
+                             int64_t o_n_emax, const uint32_t* o_tile_off, const uint32_t* o_tile_ent,
+                             const uint8_t* o_tile_sat, int64_t o_out_f, uint16_t* o_y, void* sync,
+                             void* sync_clear, int64_t sync_bytes, bf16x_stream_t stream);
+
 /* Greedy step: token[0] = argmax(logits[0 .. vocab)) (the first maximum),
  * history[state[1]] = token[0] when state[1] < history_len, then state[1]++
  * and state[0]++.  logits 16-byte aligned. */

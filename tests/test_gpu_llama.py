@@ -238,6 +238,79 @@ def test_attention_decode_matches_two_launch_path(bx, H, KV, pos, L, split, tune
 
 
 @torch.no_grad()
+@pytest.mark.parametrize("H,KV,in_f,L,mode,o_out_f", [(32, 8, 4096, 640, "exact", 4096),
+                                                       (32, 8, 4096, 768, "saturated", 4100),
+                                                       (32, 8, 4096, 300, "exact", 0), (16, 2, 3072, 300, "exact", 0),
+                                                       (64, 8, 4096, 257, "exact", 0),
+                                                       (8, 8, 2080, 512, "saturated", 0)])
+def test_layer_front_matches_separate_launches(bx, H, KV, in_f, L, mode, o_out_f):
+    """bf16x_layer_front_decode (the qkv GEMV, the decode attention and the
+    o GEMV with the residual add in one launch, ordered by device counters)
+    against bf16x_gemv_prenormed, bf16x_attention_decode and
+    bf16x_gemv_residual in sequence: qkv, the attention output, both caches,
+    the o output, the residual and its slots bit-identical, over consecutive
+    calls at several positions that alternate between two counter buffers,
+    each call clearing the other's (the timeout flag stays clear)."""
+    import types
+    from bfloat16x_amd import ops
+    from tests.test_gpu_dict import bits_tensor, to_dev
+    print("layer front", H, KV, in_f, L, mode, o_out_f, flush=True)
+    out_f = (H + 2 * KV) * 128
+    assert llama.layer_front_supported(H, KV, L, out_f, in_f)
+
+    def module(of, seed):
+        d = bx.bf16x_quantize(bits_tensor(dc.bench_weight_bits(of, in_f, seed=seed)))
+        g = to_dev(d)
+        plan = bx.build_plan_host(d, device=DEV) if mode == "exact" else None
+        return types.SimpleNamespace(_sign=g["sign_packed"], _mant=g["mant_packed"], _delta=g["delta_packed"],
+                                     _emax=g["emax"], _plan=plan, out_features=of, in_features=in_f)
+
+    def streams(m):
+        return m._sign, m._mant, m._delta, m._emax
+
+    mq = module(out_f, in_f + L)
+    mo = module(o_out_f, 7) if o_out_f else None
+    w = (1.0 + 0.1 * rnd(in_f, 3).float()).to(torch.bfloat16).to(DEV)
+    n_slots = 37
+    kc0, vc0 = rnd((KV, L, 128), 14), rnd((KV, L, 128), 15)
+    kA, vA, kB, vB = kc0.to(DEV), vc0.to(DEV), kc0.to(DEV), vc0.to(DEV)
+    cs = llama.rope_table(L, 5e5, DEV)
+    ws = llama.attention_decode_workspace(H, KV, L, DEV)
+    sync = llama.layer_front_sync(DEV, 2)
+    qA = torch.empty(out_f, dtype=torch.bfloat16, device=DEV)
+    qB = torch.full_like(qA, float("nan"))
+    oA = torch.empty(H * 128, dtype=torch.bfloat16, device=DEV)
+    oB = torch.full_like(oA, float("nan"))
+    if o_out_f:
+        n_res = ops.gemv_residual_slots(o_out_f, in_f)
+        res = rnd(o_out_f, 4).to(DEV)
+        yA, yB = (torch.empty(o_out_f, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+        rA, rB = (torch.empty(o_out_f, dtype=torch.bfloat16, device=DEV) for _ in range(2))
+        sA, sB = (torch.full((n_res + 2,), float("nan"), device=DEV) for _ in range(2))
+    for call, pos in enumerate((L - 1, L // 2, 0, L // 2)):
+        h = rnd(in_f, 20 + call).to(DEV)
+        slots = (torch.rand(n_slots, generator=torch.Generator().manual_seed(call)) * in_f / n_slots).to(DEV)
+        p = torch.tensor([pos], dtype=torch.int32, device=DEV)
+        ops.bf16x_gemv_prenormed(h, w, 1e-5, slots, n_slots, *streams(mq), out_f, in_f, plan=mq._plan, out=qA)
+        llama.attention_decode(qA, p, cs, H, KV, kA, vA, oA, ws)
+        o = None
+        if o_out_f:
+            ops.bf16x_gemv_residual(oA, res, rA, sA, *streams(mo), o_out_f, in_f, plan=mo._plan, out=yA)
+            o = (mo, res, rB, sB, yB)
+        llama.layer_front_decode(h, w, 1e-5, slots, n_slots, mq, p, cs, H, KV, kB, vB, qB, oB, sync[call % 2],
+                                 sync[1 - call % 2], o=o)
+        torch.cuda.synchronize()
+        assert not sync[1 - call % 2].any(), call                     # the other buffer cleared
+        assert int(sync[call % 2][1024]) == 0, call                   # no wait ran out
+        assert torch.equal(qB, qA), call
+        assert torch.equal(oB, oA), call
+        assert torch.equal(kB, kA) and torch.equal(vB, vA), call
+        if o_out_f:
+            assert torch.equal(yB, yA) and torch.equal(rB, rA), call
+            assert torch.equal(sB[:n_res], sA[:n_res]) and torch.isnan(sB[n_res:]).all(), call
+
+
+@torch.no_grad()
 @pytest.mark.parametrize("pairs8", [False, True])
 def test_silu_mul(bx, pairs8):
     T, F = 3, 1536
@@ -488,6 +561,33 @@ def test_residual_norm_decode_matches_prefill_and_unfused(small):
     assert not r3.res_norm and not r3.fused_norm
     r3.generate(ids.to(DEV), 6, graph=False)
     assert norm_rel(last, r3.logits.float().cpu().numpy()) < 1e-2
+
+
+MID = llama.LlamaConfig(n_layers=3, hidden=4096, ffn=1024, n_heads=32, n_kv_heads=8, vocab=1000)
+
+
+@torch.no_grad()
+def test_layer_front_decode_step(bx):
+    """A 3-layer stack of configuration-4 width with a 300-row cache: the
+    decode step whose qkv GEMV, attention and o GEMV are one launch per layer
+    (the default) gives the same tokens and bit-identical logits as the step
+    with separate launches, eager and over HIP-graph replays."""
+    mx = llama.LlamaStack(MID, device=DEV, seed=5, std=0.02)
+    bx.deploy_bf16x_fused(mx, verbose=False)
+    ids = torch.randint(0, MID.vocab, (40,), generator=torch.Generator().manual_seed(1)).to(DEV)
+    ra = llama.LlamaRunner(mx, max_len=300, max_new=10, max_prompt=64)
+    rb = llama.LlamaRunner(mx, max_len=300, max_new=10, max_prompt=64, layer_front=False)
+    assert ra.front and not rb.front
+    ta = ra.generate(ids, 10, graph=False)
+    la = ra.logits.clone()
+    tb = rb.generate(ids, 10, graph=False)
+    assert ta == tb and torch.equal(la, rb.logits)
+    ra.capture()
+    for rep in range(3):
+        torch.cuda.synchronize()
+        assert ra.generate(ids, 10, graph=True) == ta, rep
+        assert torch.equal(ra.logits, la), rep
+        assert not ra.front_sync[:, 1024].any()
 
 
 @torch.no_grad()

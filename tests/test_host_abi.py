@@ -162,6 +162,37 @@ def test_gpu_entry_points_validate_before_launch():
                           None) == _lib.ESHAPE
     assert lib.bf16x_gemv(fake, 0, fake, ws, fake, wm, fake, wd, fake, ne, None, None, None, 0, 64, 16, 1, fake,
                           None) == _lib.ESHAPE
+    # the layer launch (qkv projection + decode attention + o projection):
+    # out_f must be the qkv rows of the heads, in_f in (2048, 4096], max_len
+    # in (256, 768], sync large enough and not its own clear buffer
+    H, KV, in_f = 32, 8, 4096
+    out_f = (H + 2 * KV) * 128
+    sb = lib.bf16x_layer_front_sync_bytes()
+    assert sb >= 4 * 1025
+
+    def words(of, inf):
+        n_ = of * inf
+        return (dc.stream_words(n_, 1), dc.stream_words(n_, 7), dc.stream_words(n_, 3), n_ // 16)
+
+    def lf(of=out_f, inf=in_f, L=640, nh=H, sync_bytes=sb, mode=1, clear=None, o_out_f=0):
+        w_ = words(of, inf)
+        o = (None,) * 3 + (0,) + (None, 0) * 4 + (None,) * 3 + (0, None)
+        if o_out_f:
+            wo = words(o_out_f, inf)
+            o = (fake, ctypes.c_void_p(8192), fake, 4096, fake, wo[0], fake, wo[1], fake, wo[2], fake, wo[3],
+                 None, None, None, o_out_f, ctypes.c_void_p(12288))
+        return lib.bf16x_layer_front_decode(fake, fake, 1e-5, fake, 16, fake, w_[0], fake, w_[1], fake, w_[2], fake,
+                                            w_[3], None, None, None, of, inf, mode, fake, fake, fake, nh, KV, 128, L,
+                                            0.088, fake, fake, fake, *o, fake, clear, sync_bytes, None)
+    assert lf(of=out_f - 128) == _lib.ESHAPE
+    assert lf(inf=2048) == _lib.ESHAPE and lf(inf=4128) == _lib.ESHAPE
+    assert lf(L=256) == _lib.ESHAPE and lf(L=769) == _lib.ESHAPE
+    assert lf(nh=36, of=(36 + 2 * KV) * 128) == _lib.ESHAPE          # heads not a multiple of 8
+    assert lf(sync_bytes=sb - 4) == _lib.ECAPACITY
+    assert lf(mode=0) == _lib.EARG                                     # exact mode without a plan
+    assert lf(clear=fake) == _lib.EARG                                 # clearing its own counters
+    # an o stage whose input is not the attention output (in_f != n_heads * 128)
+    assert lf(o_out_f=4096, nh=16, of=(16 + 2 * KV) * 128) == _lib.ESHAPE
 
 
 def test_wrappers_refuse_cpu_tensors():
