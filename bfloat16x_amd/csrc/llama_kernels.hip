@@ -1128,16 +1128,18 @@ __device__ __forceinline__ void attn_decode1_body(const uint16_t* __restrict__ q
       }
       const float mn = fmaxf(m[h], mb);
       const float f = mn == -INFINITY ? 1.f : __expf(m[h] - mn);        // m = -inf: nothing to rescale
-      if (q4 == 0) pw[w][h][kg] = sc[h] == -INFINITY ? 0.f : __expf(sc[h] - mn);
-      l[h] *= f;
+      const float pe = sc[h] == -INFINITY ? 0.f : __expf(sc[h] - mn);
+      if (q4 == 0) pw[w][h][kg] = pe;
+      // each key's first lane sums its own probability; the wave's lanes are
+      // added once, at the end
+      l[h] = fmaf(l[h], f, q4 == 0 ? pe : 0.f);
       acc[h][0] *= f;
       acc[h][1] *= f;
       m[h] = mn;
     }
     __builtin_amdgcn_wave_barrier();
     // P.V over the wave's 16 keys, lane l dims 2l, 2l + 1 (a key at or past
-    // n_old is the new value row: held in LDS; past the end its p is 0), and
-    // the sum of the probabilities
+    // n_old is the new value row: held in LDS; past the end its p is 0)
     const float vn0 = vp[2 * lane], vn1 = vp[2 * lane + 1];
     float v0[16], v1[16];
 #pragma unroll
@@ -1148,19 +1150,16 @@ __device__ __forceinline__ void attn_decode1_body(const uint16_t* __restrict__ q
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      float lsum = 0.f;
 #pragma unroll
       for (int u4 = 0; u4 < 16; u4 += 4) {
         const float4 pr4 = *(const float4*)&pw[w][h][u4];
         const float pr[4] = {pr4.x, pr4.y, pr4.z, pr4.w};
-        lsum += (pr[0] + pr[1]) + (pr[2] + pr[3]);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           acc[h][0] = fmaf(pr[u], v0[u4 + u], acc[h][0]);
           acc[h][1] = fmaf(pr[u], v1[u4 + u], acc[h][1]);
         }
       }
-      l[h] += lsum;
     }
     __builtin_amdgcn_wave_barrier();
     if constexpr (NB == 0) {
@@ -1183,11 +1182,12 @@ __device__ __forceinline__ void attn_decode1_body(const uint16_t* __restrict__ q
   }
 
   // combine the waves in wave order
-  if (lane == 0) {
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
+  for (int h = 0; h < G; ++h) {
+    const float lw = wave_sum_dpp(l[h]);                         // lane 63: the wave's sum
+    if (lane == 63) {
       wm[w][h] = m[h];
-      wl[w][h] = l[h];
+      wl[w][h] = lw;
     }
   }
 #pragma unroll
