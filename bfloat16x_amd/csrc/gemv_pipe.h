@@ -45,16 +45,21 @@ __device__ __forceinline__ void load_x_atom(const void* __restrict__ x, int64_t 
   }
 }
 
+// Dot of an atom's 16 decoded pair words with bf16 x in pair order.
+__device__ __forceinline__ void dot_pairs_bf16(const uint32_t* w, const uint32_t* xr, float& acc0, float& acc1) {
+#pragma unroll
+  for (int j = 0; j < 16; j += 2) {
+    acc0 = dot2_bf16(w[j], xr[j], acc0);
+    acc1 = dot2_bf16(w[j + 1], xr[j + 1], acc1);
+  }
+}
+
 template <int XT>
 __device__ __forceinline__ void dot_atom(const Atom& t, const uint32_t* xr, float& acc0, float& acc1) {
   uint32_t w[16];
   decode_pairs(t, w);
   if constexpr (XT == BF16X_BF16) {
-#pragma unroll
-    for (int j = 0; j < 16; j += 2) {
-      acc0 = dot2_bf16(w[j], xr[j], acc0);
-      acc1 = dot2_bf16(w[j + 1], xr[j + 1], acc1);
-    }
+    dot_pairs_bf16(w, xr, acc0, acc1);
   } else {
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -304,10 +309,11 @@ __device__ __forceinline__ void gemv_pipe_body(
     load_off(rn, ebn, een);
   }
   [[maybe_unused]] uint32_t rin_pre[2] = {0u, 0u};
+  [[maybe_unused]] uint32_t wdec[PRE::active ? 2 : 1][PRE::active ? NS : 1][16];
   if constexpr (PRE::active) {
     // x comes from other workgroups of this launch: the wave's rows (iters
-    // <= 2), their entries and residuals are in flight while the workgroup
-    // waits for it
+    // <= 2), their entries and residuals are requested and the rows decoded
+    // while the workgroup waits for it
     load_row(r, bufA);
     if (iters == 2) load_row(rn, bufB);
     if constexpr (EXACT) {
@@ -317,6 +323,12 @@ __device__ __forceinline__ void gemv_pipe_body(
     if constexpr (RES == 1) {
       rin_pre[0] = ra.res_in[min(r, out_f - 1)];
       rin_pre[1] = ra.res_in[min(rn, out_f - 1)];
+    }
+#pragma unroll
+    for (int s = 0; s < NS; ++s) decode_pairs(bufA[s], wdec[0][s]);
+    if (iters == 2) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) decode_pairs(bufB[s], wdec[1][s]);
     }
     pre();
   }
@@ -456,7 +468,16 @@ __device__ __forceinline__ void gemv_pipe_body(
         const u32x4 v = xl[(s * NC + c) * 64];
         xr[4 * c] = v.x; xr[4 * c + 1] = v.y; xr[4 * c + 2] = v.z; xr[4 * c + 3] = v.w;
       }
-      if constexpr (FULL) {
+      if constexpr (PRE::active) {      // rows decoded before the wait
+        if constexpr (FULL) {
+          dot_pairs_bf16(wdec[it & 1][s], xr, acc0, acc1);
+        } else {
+          float t0 = 0.f, t1 = 0.f;
+          dot_pairs_bf16(wdec[it & 1][s], xr, t0, t1);
+          acc0 += live[s] ? t0 : 0.f;
+          acc1 += live[s] ? t1 : 0.f;
+        }
+      } else if constexpr (FULL) {
         dot_atom<XT>(cur[s], xr, acc0, acc1);
       } else {
         float t0 = 0.f, t1 = 0.f;
