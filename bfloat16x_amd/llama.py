@@ -47,7 +47,7 @@ from . import _lib, ops
 
 __all__ = ["LlamaConfig", "LlamaStack", "LlamaRunner", "rope_table", "rmsnorm", "rope_kv", "attention", "pairs8_rows",
            "attention_decode", "attention_decode_supported", "attention_decode_workspace", "layer_front_decode",
-           "layer_front_supported", "layer_front_sync", "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
+           "layer_front_supported", "layer_front_sync", "layer_front_buffers", "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
 
 NORM_ADD, NORM_STORE = 1, 2
 HEAD_DIM = 128
@@ -216,6 +216,16 @@ def layer_front_sync(device, n: int = 1) -> torch.Tensor:
     words = int(_lib.lib().bf16x_layer_front_sync_bytes()) // 4
     words = -(-words // 4) * 4                                   # rows 16-byte aligned
     return torch.zeros(n, words, dtype=torch.int32, device=device)
+
+
+def layer_front_buffers(n_launches: int) -> list:
+    """Counter buffer of each of the n_launches layer launches of a decode
+    step (n_launches >= 2): launch k uses buffer c[k] and clears c[k - 1]
+    (cyclically: the step repeats), so c[k] != c[k - 1] for every k,
+    including c[0] != c[-1]; three buffers cover any count."""
+    if n_launches < 2:
+        raise ValueError("a decode step needs at least two layer launches (each clears its predecessor's counters)")
+    return [k % 2 for k in range(n_launches - 1)] + [2]
 
 
 def _dict_args(mod):
@@ -456,8 +466,7 @@ class LlamaRunner:
             lay0.o.in_features == lay0.qkv.in_features
         if self.front:
             self.front_sync = layer_front_sync(dev, 3)
-            n_f = cfg.n_layers - 1
-            self.front_buf = [(k % 2) if k < n_f - 1 else 2 for k in range(n_f)]
+            self.front_buf = layer_front_buffers(cfg.n_layers - 1)
         self._prompt_len = 0
 
     def _decode_fused(self, pos: torch.Tensor, ids: torch.Tensor):

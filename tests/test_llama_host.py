@@ -122,3 +122,18 @@ def test_pairs8_rows_is_the_grouped_permutation():
                              8, 9, 10, 11, 24, 25, 26, 27, 12, 13, 14, 15, 28, 29, 30, 31]
     big = llama.pairs8_rows(14336)
     assert torch.equal(torch.sort(big).values, torch.arange(2 * 14336))
+
+
+@pytest.mark.parametrize("n", [2, 3, 4, 5, 31, 32, 79])
+def test_layer_front_buffers_alternate_cyclically(n):
+    """Each layer launch clears the counters of the launch before it, so no
+    two cyclically consecutive launches of a decode step (the graph repeats
+    it) may share a buffer; three buffers suffice for any count."""
+    c = llama.layer_front_buffers(n)
+    assert len(c) == n and set(c) <= {0, 1, 2}
+    assert all(c[k] != c[k - 1] for k in range(n))
+
+
+def test_layer_front_buffers_need_two_launches():
+    with pytest.raises(ValueError):
+        llama.layer_front_buffers(1)
