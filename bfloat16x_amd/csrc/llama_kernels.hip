@@ -547,20 +547,36 @@ __device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
   }
 }
 
+// Greedy argmax over kGreedyBlocks workgroups: workgroup b scans logits
+// [b span, (b + 1) span) (span a multiple of 8), its thread 0 publishes the
+// workgroup's best (value, index) and counts itself; the last one to count
+// (a device-scope counter it puts back to zero) reduces the partial results
+// across its first wave and writes the token, the history entry and the state.
+// The (value, then lower index) order makes the result the first maximum
+// whatever the order.  One launch at a time per device (the partials and the
+// counter are one device-wide set).
+constexpr int kGreedyBlocks = 32;
+__device__ uint32_t g_greedy_count;
+__device__ float g_greedy_val[kGreedyBlocks];
+__device__ int g_greedy_idx[kGreedyBlocks];
+
 __global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t* __restrict__ logits, int V,
                                                       int64_t* __restrict__ token, int32_t* __restrict__ state,
                                                       int32_t* __restrict__ hist, int hist_len) {
   __shared__ float rv[16];
   __shared__ int ri[16];
+  __shared__ bool last;
   float bv = -INFINITY;
   int bi = 0x7FFFFFFF;
-  const int tid = threadIdx.x;
-  const int full = V & ~7;
-  // 16 chunks of 8 logits per thread requested before any is compared (a
-  // 128256-entry vocabulary is one batch: one memory round trip instead of
-  // sixteen), then compared in index order
-  constexpr int kBatch = 16;
-  for (int base = tid * 8; base < full; base += 1024 * 8 * kBatch) {
+  const int tid = threadIdx.x, b = (int)blockIdx.x;
+  const int span = ((V + 8 * kGreedyBlocks - 1) / (8 * kGreedyBlocks)) * 8;
+  const int lo = min(b * span, V), hi = min(lo + span, V);
+  const int full = lo + ((hi - lo) & ~7);
+  // kBatch 8-logit groups per thread requested before any is compared (a
+  // range of up to 16384 logits is one memory round trip), then compared in
+  // index order
+  constexpr int kBatch = 2;
+  for (int base = lo + tid * 8; base < full; base += 1024 * 8 * kBatch) {
     u32x4 v[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -581,7 +597,7 @@ __global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t* __restrict
       }
     }
   }
-  if (tid < V - full) better(bv, bi, bfv(logits[full + tid]), full + tid);
+  if (tid < hi - full) better(bv, bi, bfv(logits[full + tid]), full + tid);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
   if ((tid & 63) == 0) {
@@ -591,13 +607,31 @@ __global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t* __restrict
   __syncthreads();
   if (tid == 0) {
     for (int k = 1; k < 16; ++k) better(bv, bi, rv[k], ri[k]);
-    if (bi == 0x7FFFFFFF) bi = 0;        // every logit NaN: token 0
-    token[0] = bi;
-    const int c = state[1];
-    if (c >= 0 && c < hist_len) hist[c] = bi;
-    state[1] = c + 1;
-    state[0] = state[0] + 1;
+    __hip_atomic_store(&g_greedy_val[b], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&g_greedy_idx[b], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = __hip_atomic_fetch_add(&g_greedy_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+           (uint32_t)(kGreedyBlocks - 1);
   }
+  __syncthreads();
+  if (!last || tid >= 64) return;
+  // the last workgroup's first wave: lane k reads workgroup k's result
+  static_assert(kGreedyBlocks <= 64, "one partial result per lane");
+  bv = -INFINITY;
+  bi = 0x7FFFFFFF;
+  if (tid < kGreedyBlocks) {
+    bv = __hip_atomic_load(&g_greedy_val[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bi = __hip_atomic_load(&g_greedy_idx[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
+  if (tid != 0) return;
+  __hip_atomic_store(&g_greedy_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (bi == 0x7FFFFFFF) bi = 0;          // every logit NaN: token 0
+  token[0] = bi;
+  const int c = state[1];
+  if (c >= 0 && c < hist_len) hist[c] = bi;
+  state[1] = c + 1;
+  state[0] = state[0] + 1;
 }
 
 }  // namespace
@@ -1529,10 +1563,11 @@ extern "C" int bf16x_greedy(const uint16_t* logits, int64_t vocab, int64_t* toke
                             int64_t history_len, bf16x_stream_t stream) {
   if (!logits || !token || !state || (!history && history_len > 0) || history_len < 0) return BF16X_EARG;
   // greedy_kernel steps its int indices by 1024 * 8 per batch element and
-  // 16 elements per batch: the last batch's indices must not overflow
-  if (vocab <= 0 || vocab > INT32_MAX - 2 * 1024 * 8 * 16 || history_len > INT32_MAX) return BF16X_ESHAPE;
+  // 2 elements per batch, its ranges by a multiple of 8: the last indices
+  // must not overflow
+  if (vocab <= 0 || vocab > INT32_MAX - 4 * 1024 * 8 * kGreedyBlocks || history_len > INT32_MAX) return BF16X_ESHAPE;
   if (!aligned16(logits) || !aligned4(state) || ((uintptr_t)token & 7u)) return BF16X_EARG;
-  hipLaunchKernelGGL(greedy_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, logits, (int)vocab, token, state,
-                     history, (int)history_len);
+  hipLaunchKernelGGL(greedy_kernel, dim3(kGreedyBlocks), dim3(1024), 0, (hipStream_t)stream, logits, (int)vocab,
+                     token, state, history, (int)history_len);
   return launch_status();
 }

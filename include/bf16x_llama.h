@@ -188,7 +188,9 @@ int bf16x_layer_front_decode(const void* h, const uint16_t* norm_weight, float e
 
 /* Greedy step: token[0] = argmax(logits[0 .. vocab)) (the first maximum),
  * history[state[1]] = token[0] when state[1] < history_len, then state[1]++
- * and state[0]++.  logits 16-byte aligned. */
+ * and state[0]++.  logits 16-byte aligned.  The launch's workgroups meet in
+ * one device-wide set of partial results: calls on one device must not
+ * overlap (stream order, one graph replay at a time). */
 int bf16x_greedy(const uint16_t* logits, int64_t vocab, int64_t* token, int32_t* state, int32_t* history,
                  int64_t history_len, bf16x_stream_t stream);
 
