@@ -62,6 +62,21 @@ def bench_weight(out_f: int, in_f: int, seed: int = 0) -> torch.Tensor:
     return w.to(torch.bfloat16)
 
 
+def check_output(y: torch.Tensor, w: torch.Tensor, x: torch.Tensor, max_tol: float = 1e-2,
+                 med_tol: float = 2e-3) -> dict:
+    """Elementwise relative error of a timed output y (= x . W^T, or W . x
+    for a vector x) against an fp64 product of the original weight on the
+    device, |y - ref| / max(|ref|, 1e-3 rms(ref)); raises when the max or
+    median exceeds the north-star tolerance.  Returns {"max", "median"}."""
+    ref = (w.double() @ x.double()) if x.dim() == 1 else (x.double() @ w.double().t().contiguous())
+    rms = ref.pow(2).mean().sqrt().item()
+    e = ((y.double() - ref).abs() / ref.abs().clamp_min(1e-3 * rms + 1e-30)).reshape(-1)
+    mx, med = e.max().item(), e.median().item()
+    if not (mx <= max_tol and med <= med_tol):
+        raise RuntimeError(f"timed output outside tolerance: rel err max {mx:.3e} median {med:.3e}")
+    return {"max": float(f"{mx:.3e}"), "median": float(f"{med:.3e}")}
+
+
 def alg_bytes_gemv(d: dict, n_fix: int) -> int:
     return (4 * (d["sign_packed"].numel() + d["mant_packed"].numel() + d["delta_packed"].numel())
             + d["emax"].numel() + 5 * n_fix + 2 * d["in_f"] + 2 * d["out_f"])
@@ -230,10 +245,9 @@ def bench_sweep(bx, dev, stream) -> dict:
         sec_b = time_launches(lambda i: torch.nn.functional.linear(xb, wcs[i % nw]), 200, 20, stream, queued=True)
         ent = {"shape": f"{out_f}x{in_f}", "us": round(sec * 1e6, 2), "GBps": round(ab / sec / 1e9, 1),
                "hbm_frac": round(ab / sec / 1e9 / HBM_PEAK_GBS, 4), "bf16_linear_us": round(sec_b * 1e6, 2),
-               "speedup_vs_bf16": round(sec_b / sec, 3)}
+               "speedup_vs_bf16": round(sec_b / sec, 3), "rel_err_vs_fp64": check_output(y, wd, x)}
         gemv_rec.append(ent)
         log(f"config2 gemv {ent}")
-        del wcs
         if (out_f, in_f) != (1024, 4096):
             for _, p in cps:
                 p.kplan()
@@ -250,13 +264,15 @@ def bench_sweep(bx, dev, stream) -> dict:
                     sg = time_launches(gm, n_l, 3, stream, queued=True)
                     e[f"{path}_us"] = round(sg * 1e6, 2)
                     e[f"{path}_tflops"] = round(flops / sg / 1e12, 1)
-                st_ = time_launches(lambda i: torch.nn.functional.linear(xm, wd), 30, 3, stream, queued=True)
+                # the bf16 comparator rotates over weight copies too (HBM-resident)
+                st_ = time_launches(lambda i: torch.nn.functional.linear(xm, wcs[i % nw]), 30, 3, stream,
+                                    queued=True)
                 e["torch_bf16_linear_us"] = round(st_ * 1e6, 2)
                 gemm_roofline(e, flops, out_f, in_f)
                 gemm_rec.append(e)
                 log(f"config3 gemm {e}")
                 del xm
-        del cps, d, plan, wd
+        del cps, d, plan, wd, wcs
         torch.cuda.empty_cache()
     return {"gemv_config2": gemv_rec, "gemm_config3": gemm_rec}
 
@@ -296,14 +312,14 @@ def bench_gguf(bx, dev, stream) -> list:
         sec_ml = time_launches(lambda i: bx.gguf.gguf_gemm(xm, copies[i % 2], out_f, in_f, ovf=ovf), 10, 2, stream)
         sec_md = time_launches(lambda i: torch.nn.functional.linear(xm, bx.gguf.gguf_decode(copies[i % 2], out_f,
                                                                                               in_f)), 10, 2, stream)
-        sec_mb = time_launches(lambda i: torch.nn.functional.linear(xm, wb), 10, 2, stream)
+        wcopies = [wb, wb.clone()]
+        sec_mb = time_launches(lambda i: torch.nn.functional.linear(xm, wcopies[i % 2]), 10, 2, stream)
         sec_lv = time_launches(lambda i: bx.gguf.gguf_gemv(x, copies[i % 2], out_f, in_f, ovf=ovf), 200, 20, stream)
         dec_l = bx.gguf.gguf_decode(copies[0], out_f, in_f, ovf=ovf)
         lossless_exact = bool(torch.equal(dec_l.view(torch.int16), wb.view(torch.int16)))
         sec_ld = time_launches(lambda i: bx.gguf.gguf_decode(copies[i % 2], out_f, in_f, out=dec_l, ovf=ovf), 30, 4,
                                stream)
         del dec_l
-        wcopies = [wb, wb.clone()]
         sec_bv = time_launches(lambda i: torch.nn.functional.linear(x.view(1, -1), wcopies[i % 2]), 100, 10, stream)
         del wcopies, wb, copies, xm
         torch.cuda.empty_cache()
@@ -413,9 +429,10 @@ def bench_llama(bx, dev, prompt_len: int = 512, n_new: int = 128, reps: int = 2)
             r.prefill(ids)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            r.decode(n_new - 1)
+            r.decode(n_new - 1, check=False)
             torch.cuda.synchronize()
             dec.append((time.perf_counter() - t0) / (n_new - 1))
+            r.check_layer_launch()                   # outside the timed region
         toks = r.history[:n_new].tolist()
         ms_tok = min(dec) * 1e3
         per_tok = linear_bytes + head_bytes + r.kv_bytes_per_step()
@@ -552,9 +569,15 @@ def main():
     def step(i):
         lib.bf16x_gemv(*argv[i % n_copies])
 
-    sec = time_launches(step, args.steps, args.warmup, stream)
+    # queued: every launch is enqueued before the first starts, so the
+    # events time the GPU's back-to-back launches, not the host's calls
+    sec = time_launches(step, args.steps, args.warmup, stream, queued=True)
     gbs = abytes / sec / 1e9
     log(f"bf16x gemv: {sec * 1e6:.2f} us/launch, {gbs:.1f} GB/s algorithmic ({n_copies} rotating copies)")
+    # the timed launches' output (every copy holds the same weight) against
+    # an fp64 product of the original weight
+    gemv_err = check_output(y, wd, x)
+    log(f"bf16x gemv output vs fp64: {gemv_err}")
     # the same launches one at a time, each between its own pair of events:
     # median and spread over 200 (the per-launch statistic; `value` is the
     # back-to-back mean above)
@@ -590,7 +613,6 @@ def main():
 
     sec_bf16 = time_launches(step_bf16, max(200, args.steps // 4), 20, stream)
     log(f"bf16 F.linear gemv: {sec_bf16 * 1e6:.2f} us ({wd.numel() * 2 / sec_bf16 / 1e9:.1f} GB/s of bf16 bytes)")
-    del wcopies
 
     # ---- device encoder at the headline shape (bf16 weight in HBM -> dict)
     wdev = w.to(dev)
@@ -637,7 +659,12 @@ def main():
             sec_g = time_launches(step_g, n_l, 3, stream, queued=True)
             ent[f"{path}_us"] = round(sec_g * 1e6, 2)
             ent[f"{path}_tflops"] = round(flops / sec_g / 1e12, 1)
-        sec_t = time_launches(lambda i: torch.nn.functional.linear(xm, wd), 30, 3, stream, queued=True)
+            g0, p0 = copies[0]
+            ent[f"{path}_rel_err_vs_fp64"] = check_output(
+                bx.bf16x_gemm(xm, g0["sign_packed"], g0["mant_packed"], g0["delta_packed"], g0["emax"], out_f, in_f,
+                              plan=p0, path=path), wd, xm)
+        sec_t = time_launches(lambda i: torch.nn.functional.linear(xm, wcopies[i % len(wcopies)]), 30, 3, stream,
+                              queued=True)
         ent["torch_bf16_linear_us"] = round(sec_t * 1e6, 2)
         gemm_roofline(ent, flops, out_f, in_f)
         gemm_rec.append(ent)
@@ -645,7 +672,7 @@ def main():
         del xm
 
     # ---- configurations 2 and 3 at every shape
-    del copies, argv
+    del copies, argv, wcopies
     torch.cuda.empty_cache()
     sweep_rec = None
     if not args.no_sweep:
@@ -689,6 +716,7 @@ def main():
         "gemv_single_launch": single_rec,
         "bf16_gemv_us": round(sec_bf16 * 1e6, 3),
         "speedup_vs_bf16_gemv": round(sec_bf16 / sec, 3),
+        "gemv_rel_err_vs_fp64": gemv_err,
         "hbm_pct": round(100 * gbs / HBM_PEAK_GBS, 2),
         "decode_exact_14336x4096": decode_rec,
         "device_encoder_14336x4096": enc_rec,

@@ -87,7 +87,8 @@ PROTOTYPES = {
                                                 _c_i64, _c_i64, _c_i64, _c_i64, ctypes.c_float, _P, _P, _P,
                                                 _P, _P, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64,
                                                 _P, _P, _P, _c_i64, _P, _P, _P, _c_i64, _P]),
-    "bf16x_greedy": (ctypes.c_int, [_P, _c_i64, _P, _P, _P, _c_i64, _P]),
+    "bf16x_greedy_workspace_bytes": (_c_i64, []),
+    "bf16x_greedy": (ctypes.c_int, [_P, _c_i64, _P, _P, _P, _c_i64, _P, _c_i64, _P]),
     # kernel-choice overrides (include/bf16x_hip.h)
     "bf16x_set_tuning": (ctypes.c_int, [_c_i32, _c_i64]),
     "bf16x_get_tuning": (_c_i64, [_c_i32]),
@@ -99,7 +100,6 @@ TUNE_KEYS = {
     "gemm_ws_split": 5, "skinny_waves": 6, "skinny2_kq": 7, "skinny2_split": 8, "gemv_iters": 9, "gemv_g": 10,
     "gemv_long": 11, "gemv_xm_slots": 12, "gguf_long": 13, "gguf_iters": 14, "attn_split": 15,
     "gemm_ws_grouped": 16, "gemm_ws_resident": 17, "attn_mfma": 18,
-    "gemm_ws5_min_rows": 19,
 }
 
 _LIB = None

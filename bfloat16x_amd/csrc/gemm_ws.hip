@@ -108,7 +108,7 @@ struct RawG {
 // share a W tile run on one XCD at the same time and share its L2.
 struct WsGrid {
   int mtiles, full, ltiles, lunits;
-  int bm;         // tokens per tile: kBM (wave-specialised kernels) or kBM5 (gemm_ws5_kernel)
+  int bm;         // tokens per tile (kBM)
 };
 struct WsWork {
   int64_t m0, n0;
@@ -770,299 +770,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   ws_store<YF32>(acc, wk, wave, lane, M, out_f, grid.ltiles, y, part);
 }
 
-// ---------------------------------------------------------------------------
-// One wave per SIMD, every wave both decodes and multiplies (in_f % 256 == 0;
-// selected by BF16X_TUNE_GEMM_WS5_MIN_ROWS, see kWs5MinRows for why it is not
-// the default): the four-step-group LDS tile of the
-// kernel above, but the workgroup is 4 waves of up to 512 registers and wave
-// w owns tokens 128 w .. 128 w + 127 of a 512-token tile (4 x 4 accumulators
-// of v_mfma_f32_32x32x16_bf16, 256 registers) and decodes W rows 32 w ..
-// 32 w + 31 of the next group, as decode wave 4 + w does above.  Measured on
-// gfx950 with one wave per SIMD: independent VALU instructions in an MFMA
-// wave's own stream mostly run under its MFMAs (32 MFMAs: 1025 cycles alone,
-// 1181 with 128 VALU, 1481 with 256), so the decode costs the MFMA waves
-// little, while each W operand read from LDS now feeds 4 token tiles instead
-// of 2: half the LDS reads per MFMA, the bound of the kernel above.  Round u
-// of the next group is decoded during step u of the current one, four pairs
-// (one 16-byte chunk) per k-quarter, the chunk's VALU interleaved with the
-// quarter's 16 MFMAs; x is loaded one step ahead, quarter by quarter, into
-// the registers the quarter's MFMAs have just read; one barrier per group.
-// ---------------------------------------------------------------------------
-constexpr int kBM5 = 512;                    // tokens per tile
-
-template <bool GG, bool EXACT, bool YF32>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gemm_ws5_kernel(
-    const uint16_t* __restrict__ x, int64_t M, const uint32_t* __restrict__ sign,
-    const uint32_t* __restrict__ mant, const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
-    const uint8_t* __restrict__ blocks, const uint32_t* __restrict__ kp_off, const uint32_t* __restrict__ kp_ent,
-    int64_t out_f, int64_t in_f, WsGrid grid, void* __restrict__ y, float* __restrict__ part) {
-  // two W slots, then 256 bytes where the plan patch lanes with no entry write
-  __shared__ __attribute__((aligned(16))) uint8_t wlds[2 * kWSlot4 + 256];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // 0..3
-
-  const int S = (int)(in_f >> 6);
-  const WsWork wk = ws_work(grid, S / kGroup);  // units are groups
-  const int64_t m0 = wk.m0, n0 = wk.n0;
-  const int g0 = wk.u0;
-  const int ng = wk.nu;                         // groups of this block (>= 1)
-
-  // ---------------- decode part: W rows 32 wave .. + 31 of the tile ----------------
-  const int64_t P = in_f >> 5;                  // atoms per row (a multiple of 8)
-  const int a = lane & 7, rq = lane >> 3;       // atom of the group, row within a round
-  using RawT = typename std::conditional<GG, RawG, Raw>::type;
-  const uint64_t wat = (uint64_t)(out_f - n0) * P;
-  __amdgpu_buffer_rsrc_t rs_, rm_, rd_, re_, rb_;
-  uint32_t vo_s = 0, vo_m = 0, vo_d = 0, vo_e = 0, vo_b = 0, sh = 0;
-  const uint32_t av = (uint32_t)((32 * wave + rq) * P) + (uint32_t)a;
-  const uint32_t rstep = (uint32_t)(8 * P);     // atoms from one round's row to the next
-  if constexpr (GG) {
-    rb_ = rsrc(blocks + (uint64_t)n0 * P * 46, (wat * 46 + 3) & ~3ull);
-    vo_b = (av * 46) & ~3u;
-    sh = 16u * (uint32_t)(a & 1);
-  } else {
-    rs_ = rsrc(sign + n0 * P, wat * 4);
-    rm_ = rsrc(mant + n0 * P * 7, wat * 28);
-    rd_ = rsrc(delta + n0 * P * 3, wat * 12);
-    re_ = rsrc(emax2 + n0 * P, wat * 2);
-    vo_s = av * 4; vo_m = av * 28; vo_d = av * 12; vo_e = (av & ~1u) * 2;
-  }
-  auto load_round = [&](int gj, int i, RawT& t) {
-    const uint32_t ra = (uint32_t)(g0 + min(gj, ng - 1)) * 8u + (uint32_t)i * rstep;
-    if constexpr (GG) {
-      t.q0 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)vo_b, (int)(ra * 46), 0);
-      t.q1 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)(vo_b + 16), (int)(ra * 46), 0);
-      t.q2 = __builtin_amdgcn_raw_buffer_load_b128(rb_, (int)(vo_b + 32), (int)(ra * 46), 0);
-    } else {
-      const u32x4 m03 = __builtin_amdgcn_raw_buffer_load_b128(rm_, (int)vo_m, (int)(ra * 28), 0);
-      const u32x3 m46 = __builtin_amdgcn_raw_buffer_load_b96(rm_, (int)(vo_m + 16), (int)(ra * 28), 0);
-      const u32x3 d02 = __builtin_amdgcn_raw_buffer_load_b96(rd_, (int)vo_d, (int)(ra * 12), 0);
-      t.s = __builtin_amdgcn_raw_buffer_load_b32(rs_, (int)vo_s, (int)(ra * 4), 0);
-      t.ew = __builtin_amdgcn_raw_buffer_load_b32(re_, (int)vo_e, (int)(ra * 2), 0);
-      const uint32_t c0 = m03.x, c1 = m03.y, c2 = m03.z, c3 = m03.w, c4 = m46.x, c5 = m46.y, c6 = m46.z;
-      t.m[0] = c0; t.m[1] = c1; t.m[2] = c2; t.m[3] = c3; t.m[4] = c4; t.m[5] = c5; t.m[6] = c6;
-      const uint32_t e0 = d02.x, e1 = d02.y, e2 = d02.z;
-      t.d[0] = e0; t.d[1] = e1; t.d[2] = e2;
-    }
-  };
-  auto prep_round = [&](const RawT& w) -> PairState {
-    if constexpr (GG) {
-      return prep_pairs(gguf_atom(GgufRaw{w.q0, w.q1, w.q2, sh}));
-    } else {
-      Atom t;
-      t.s = w.s;
-#pragma unroll
-      for (int k = 0; k < 7; ++k) t.m[k] = w.m[k];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) t.d[k] = w.d[k];
-      t.e = (uint16_t)(w.ew >> (16 * (a & 1)));
-      return prep_pairs(t);
-    }
-  };
-  // chunk c (pairs 4c .. 4c+3) of round i's atom into slot `slot`
-  auto store_chunk = [&](const PairState& q, int i, int c, int slot) {
-    const int r = 32 * wave + 8 * i + rq;
-    uint8_t* row = wlds + slot * kWSlot4 + r * kRowB4;
-    *(u32x4*)(row + swz4(r, 4 * a + c) * 16) =
-        u32x4{decode_pair<GG>(q, 4 * c), decode_pair<GG>(q, 4 * c + 1), decode_pair<GG>(q, 4 * c + 2),
-              decode_pair<GG>(q, 4 * c + 3)};
-  };
-
-  // EXACT plan: the runs of this wave's 32-row group at the 4 steps of a group
-  const int64_t G = (out_f + 31) / 32, G2 = 2 * G;
-  const int64_t gr = min(n0 / 32 + wave, G);
-  uint32_t kp_total = 0;
-  if constexpr (EXACT) kp_total = kp_off[S * G2];
-  const __amdgpu_buffer_rsrc_t rent = rsrc(kp_ent, (uint64_t)kp_total * 4);
-  const __amdgpu_buffer_rsrc_t roff = rsrc(kp_off, ((uint64_t)S * G2 + 1) * 4);
-  const uint32_t ob = (uint32_t)(2 * gr) * 4, oe = (uint32_t)min(2 * gr + 2, G2) * 4;
-  struct Off { uint32_t beg[kGroup], end[kGroup]; };
-  struct Ent { uint32_t beg[kGroup], end[kGroup], e0[kGroup], e1[kGroup]; };
-  auto load_off = [&](int gj, Off& o) {
-    const uint32_t s0_ = (uint32_t)(g0 + min(gj, ng - 1)) * kGroup;
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) {
-      o.beg[u] = __builtin_amdgcn_raw_buffer_load_b32(roff, (int)ob, (int)((s0_ + u) * G2 * 4), 0);
-      o.end[u] = __builtin_amdgcn_raw_buffer_load_b32(roff, (int)oe, (int)((s0_ + u) * G2 * 4), 0);
-    }
-  };
-  auto load_ent = [&](const Off& o, Ent& e) {
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) {
-      e.beg[u] = __builtin_amdgcn_readfirstlane(o.beg[u]);
-      e.end[u] = __builtin_amdgcn_readfirstlane(o.end[u]);
-      e.e0[u] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((e.beg[u] + lane) * 4), 0, 0);
-      e.e1[u] = __builtin_amdgcn_raw_buffer_load_b32(rent, (int)((e.beg[u] + lane + 64) * 4), 0, 0);
-    }
-  };
-  auto patch_one = [&](uint32_t e, int slot, int u, bool live) {
-    const int rr = (int)(e >> 22) & (kBN - 1), c = (int)(e >> 16) & 63;
-    const uint32_t dst =
-        (uint32_t)(slot * kWSlot4 + rr * kRowB4 + swz4(rr, 8 * u + chunk_of(c)) * 16 + pos_of(c) * 2);
-    __asm__ volatile("" : "+v"(e));
-    *(uint16_t*)(wlds + (live ? dst : (uint32_t)(2 * kWSlot4 + lane * 4))) = (uint16_t)(e & 0xFFFFu);
-  };
-  auto patch = [&](const Ent& e, int slot) {
-    uint32_t longest = 0;
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) {
-      patch_one(e.e0[u], slot, u, e.beg[u] + lane < e.end[u]);
-      longest = max(longest, e.end[u] - e.beg[u]);
-    }
-    if (longest > 64) {
-#pragma unroll
-      for (int u = 0; u < kGroup; ++u) {
-        if (e.beg[u] + lane + 64 < e.end[u]) patch_one(e.e1[u], slot, u, true);
-        for (uint32_t k = e.beg[u] + 128 + lane; k < e.end[u]; k += 64)   // dense runs
-          patch_one(kp_ent[k], slot, u, true);
-      }
-    }
-  };
-
-  // ---------------- MFMA part: tokens 128 wave .. + 127, all 128 W rows ----------------
-  const int lr = lane & 31, h = lane >> 5;
-  const int n = ng * kGroup;                    // steps of this block
-  const int s0 = g0 * kGroup;
-  const int64_t S64 = S;
-  const __amdgpu_buffer_rsrc_t rx_ = rsrc(x + m0 * in_f, (uint64_t)(((M + 31) / 32) * 32 - m0) * (uint64_t)in_f * 2);
-  uint32_t vx[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) vx[i] = (uint32_t)((4 * wave + i) * S64 * 4096 + lane * 16);
-  // x of k-quarter q of block step jx for the 4 token tiles
-  auto load_xq = [&](int jx, int q, bf16x8_t (&X)[4]) {
-    const uint32_t ks = (uint32_t)(s0 + min(jx, n - 1)) * 4096;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      X[i] = __builtin_bit_cast(bf16x8_t, __builtin_amdgcn_raw_buffer_load_b128(rx_, (int)(vx[i] + q * 1024),
-                                                                                  (int)ks, 0));
-  };
-  uint32_t wo[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q) wo[q] = (uint32_t)(lr * kRowB4 + (((4 * h + q) ^ (lr & 15)) * 16));
-  auto load_w = [&](int q, int u, int slot, bf16x8_t (&wb)[4]) {
-    const uint32_t ku = (uint32_t)(((8 * u) ^ ((u >> 1) << 1)) * 16) | ((uint32_t)slot << 16);
-    const uint32_t o = wo[q] ^ ku;
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) wb[jj] = *(const bf16x8_t*)(wlds + o + jj * 32 * kRowB4);
-  };
-  f32x16 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][jj][v] = 0.f;
-
-  // two rounds of atoms in registers: R[u & 1] holds the round decoded at
-  // step u, then takes the round decoded two steps later
-  RawT R[2];
-  Off O{};
-  Ent E{};
-  bf16x8_t X[4][4], W0[4], W1[4];
-
-  // prologue: plan of groups 0 (entries) and 1 (offsets), group 0 decoded
-  // into slot 0 round by round, x of step 0; R then holds rounds 0 and 1 of
-  // group 1
-  if constexpr (EXACT) load_off(0, O);
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (EXACT) { load_ent(O, E); load_off(1, O); }
-  load_round(0, 0, R[0]);
-  load_round(0, 1, R[1]);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) load_xq(0, q, X[q]);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const PairState ps = prep_round(R[i & 1]);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) store_chunk(ps, i, c, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_round(i < 2 ? 0 : 1, (i + 2) & 3, R[i & 1]);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if constexpr (EXACT) {
-    patch(E, 0);
-    __builtin_amdgcn_sched_barrier(0);
-    load_ent(O, E);
-    load_off(2, O);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  __syncthreads();
-  load_w(0, 0, 0, W0);
-
-#define BF16X_SG(mask, cnt) __builtin_amdgcn_sched_group_barrier(mask, cnt, 0)
-  // 16 MFMAs of k-quarter q (x operands Xq, W operands wb)
-  auto mfma16 = [&](const bf16x8_t (&Xq)[4], const bf16x8_t (&wb)[4]) {
-#pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int i = t >> 2, jj = t & 3;
-      acc[i][jj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(Xq[i], wb[jj], acc[i][jj], 0, 0, 0);
-    }
-  };
-  // one k-quarter: the next quarter's W operands requested first, then the
-  // 16 MFMAs with chunk c of the round being decoded spread between them,
-  // then x of the next step for this quarter into the registers just read
-  auto quarter = [&](int jx, int q, const bf16x8_t (&wb)[4], const PairState& ps, int u, int slot_n) {
-    mfma16(X[q], wb);
-    store_chunk(ps, u, q, slot_n);
-    load_xq(jx + 1, q, X[q]);
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      BF16X_SG(0x008, 1);
-      BF16X_SG(0x002, 3);
-    }
-    BF16X_SG(0x200, 1);
-    BF16X_SG(0x020, 4);
-    __builtin_amdgcn_sched_barrier(0);
-  };
-  // step u of group j (block step jx) from slot `slot`; round u of group
-  // j + 1 decoded into the other slot meanwhile, its registers then refilled
-  // with the round decoded two steps later (round u + 2 of group j + 1, or
-  // round u - 2 of group j + 2)
-  auto step = [&](int j, int u, int slot) {
-    const int jx = kGroup * j + u;
-    load_w(1, u, slot, W1);
-    __builtin_amdgcn_sched_barrier(0);
-    const PairState ps = prep_round(R[u & 1]);  // in quarter 0's region: its VALU runs under the MFMAs
-    quarter(jx, 0, W0, ps, u, slot ^ 1);
-    load_w(2, u, slot, W0);
-    __builtin_amdgcn_sched_barrier(0);
-    quarter(jx, 1, W1, ps, u, slot ^ 1);
-    load_w(3, u, slot, W1);
-    __builtin_amdgcn_sched_barrier(0);
-    quarter(jx, 2, W0, ps, u, slot ^ 1);
-    if (u < kGroup - 1) load_w(0, u + 1, slot, W0);
-    __builtin_amdgcn_sched_barrier(0);
-    quarter(jx, 3, W1, ps, u, slot ^ 1);
-    load_round(u < 2 ? j + 1 : j + 2, (u + 2) & 3, R[u & 1]);
-    __builtin_amdgcn_sched_barrier(0);
-    if (u == kGroup - 1) {
-      if constexpr (EXACT) {
-        patch(E, slot ^ 1);
-        __builtin_amdgcn_sched_barrier(0);
-        load_ent(O, E);
-        load_off(j + 3, O);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      __syncthreads();
-      load_w(0, 0, slot ^ 1, W0);
-    }
-  };
-#undef BF16X_SG
-  int j = 0;
-  for (; j + 1 < ng; j += 2) {
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) step(j, u, 0);
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) step(j + 1, u, 1);
-  }
-  if (j < ng) {
-#pragma unroll
-    for (int u = 0; u < kGroup; ++u) step(j, u, 0);
-  }
-  ws_store<YF32, 4>(acc, wk, wave, lane, M, out_f, grid.ltiles, y, part);
-}
-
 // x [M, K] -> operand order: 32-row tile T, step s (64 columns), k-quarter q
 // is 1 KB at ((T * S + s) * 4 + q) * 1024, lane l = lr + 32 h holding row
 // 32 T + lr, columns 64 s + 32 h + {4q, 16+4q, 4q+1, 17+4q, .., 4q+3, 19+4q}
@@ -1124,7 +831,6 @@ struct WsShape {
   int nsplit;       // K ranges of a split tile (1: no split tiles)
   int64_t grid;     // blocks
   bool grouped;     // four-step-group kernel (units are groups, else steps)
-  bool ws5;         // gemm_ws5_kernel (512-token tiles, one wave per SIMD)
 };
 
 // Four-step groups when K allows (the grouped kernel reads W in runs of
@@ -1154,27 +860,10 @@ int64_t ws_resident() {
 // only for those 128 tiles.  BF16X_TUNE_GEMM_WS_SPLIT > 0 splits every tile
 // into that many K ranges instead; BF16X_TUNE_GEMM_WS_RESIDENT > 0 replaces
 // the resident block count (tests reach the mixed plan with few tiles).
-// gemm_ws5_kernel from this many rows on (four-step groups only): 0, i.e.
-// only when the override BF16X_TUNE_GEMM_WS5_MIN_ROWS selects it.  Measured
-// against gemm_ws4_kernel (exact, weights rotated through HBM, us): 14336x4096
-// M = 512 / 1024 / 2048: 106 / 162 / 308 against 83 / 172 / 301; 4096x14336
-// M = 2048: 274 against 270; 28672x4096 M = 1024: 298 against 299.  A copy
-// reduced to its MFMAs and barriers (no loads, no decode, no LDS) still took
-// 207 us at 14336x4096 M = 2048 (hipBLASLt on the decoded weight: 194-209
-// us): at these sizes the matrix cores run power-limited, so the halved LDS
-// reads and decode per MFMA turn into clock, not time.
-constexpr int64_t kWs5MinRows = 0;
-bool ws5_use(int64_t M, int64_t in_f) {
-  const int64_t t = tuning(BF16X_TUNE_GEMM_WS5_MIN_ROWS);
-  const int64_t min_rows = t >= 0 ? t : kWs5MinRows;
-  return ws_grouped(in_f) && min_rows > 0 && M >= min_rows;
-}
-
 WsShape ws_shape(int64_t M, int64_t out_f, int64_t in_f) {
   WsShape w;
   w.grouped = ws_grouped(in_f);
-  w.ws5 = ws5_use(M, in_f);
-  const int64_t bm = w.ws5 ? kBM5 : kBM;
+  const int64_t bm = kBM;
   const int64_t mt = (M + bm - 1) / bm, nt = (out_f + kBN - 1) / kBN;
   const int64_t S = in_f / kStep, tiles = mt * nt;
   const int64_t units = w.grouped ? S / kGroup : S;
@@ -1236,10 +925,7 @@ int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const 
   const dim3 grid((unsigned)w.grid);
 #define BF16X_WS1(GG_, EX_, YF_)                                                                                   \
   do {                                                                                                           \
-    if (w.ws5)                                                                                                   \
-      hipLaunchKernelGGL((gemm_ws5_kernel<GG_, EX_, YF_>), grid, dim3(256), 0, st, xo, M, s, m, d, e, blocks,       \
-                         kp_off, kp_ent, out_f, in_f, w.g, y, part);                                              \
-    else if (w.grouped)                                                                                          \
+    if (w.grouped)                                                                                               \
       hipLaunchKernelGGL((gemm_ws4_kernel<GG_, EX_, YF_>), grid, dim3(512), 0, st, xo, M, s, m, d, e, blocks,       \
                          kp_off, kp_ent, out_f, in_f, w.g, y, part);                                              \
     else                                                                                                         \

@@ -40,6 +40,18 @@ inline int check_dict(int64_t out_f, int64_t in_f, int32_t sub, int64_t n_sign, 
   return BF16X_OK;
 }
 
+// Compute units of the current device (cached per device), or 0 when it
+// cannot be queried.
+inline int device_cus() {
+  static int cache[64];
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] > 0) return cache[dev];
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+  cache[dev] = cus;
+  return cus;
+}
+
 inline int tiles_per_row(int64_t in_f) { return (int)((in_f + kPlanTileCols - 1) / kPlanTileCols); }
 
 }  // namespace

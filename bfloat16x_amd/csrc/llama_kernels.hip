@@ -553,16 +553,21 @@ __device__ __forceinline__ void better(float& v, int& i, float v2, int i2) {
 // (a device-scope counter it puts back to zero) reduces the partial results
 // across its first wave and writes the token, the history entry and the state.
 // The (value, then lower index) order makes the result the first maximum
-// whatever the order.  One launch at a time per device (the partials and the
-// counter are one device-wide set).
+// whatever the order.  The counter and the partial results live in the
+// caller's workspace (GreedyWs): launches with different workspaces are
+// independent; launches that share one must not overlap.
 constexpr int kGreedyBlocks = 32;
-__device__ uint32_t g_greedy_count;
-__device__ float g_greedy_val[kGreedyBlocks];
-__device__ int g_greedy_idx[kGreedyBlocks];
+struct GreedyWs {
+  uint32_t count;                 // zero between launches (the last workgroup puts it back)
+  uint32_t pad[63];
+  float val[kGreedyBlocks];
+  int idx[kGreedyBlocks];
+};
 
 __global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t* __restrict__ logits, int V,
                                                       int64_t* __restrict__ token, int32_t* __restrict__ state,
-                                                      int32_t* __restrict__ hist, int hist_len) {
+                                                      int32_t* __restrict__ hist, int hist_len,
+                                                      GreedyWs* __restrict__ ws) {
   __shared__ float rv[16];
   __shared__ int ri[16];
   __shared__ bool last;
@@ -607,9 +612,9 @@ __global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t* __restrict
   __syncthreads();
   if (tid == 0) {
     for (int k = 1; k < 16; ++k) better(bv, bi, rv[k], ri[k]);
-    __hip_atomic_store(&g_greedy_val[b], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&g_greedy_idx[b], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = __hip_atomic_fetch_add(&g_greedy_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+    __hip_atomic_store(&ws->val[b], bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&ws->idx[b], bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = __hip_atomic_fetch_add(&ws->count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
            (uint32_t)(kGreedyBlocks - 1);
   }
   __syncthreads();
@@ -619,13 +624,13 @@ __global__ __launch_bounds__(1024) void greedy_kernel(const uint16_t* __restrict
   bv = -INFINITY;
   bi = 0x7FFFFFFF;
   if (tid < kGreedyBlocks) {
-    bv = __hip_atomic_load(&g_greedy_val[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    bi = __hip_atomic_load(&g_greedy_idx[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bv = __hip_atomic_load(&ws->val[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    bi = __hip_atomic_load(&ws->idx[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) better(bv, bi, __shfl_xor(bv, o, 64), __shfl_xor(bi, o, 64));
   if (tid != 0) return;
-  __hip_atomic_store(&g_greedy_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&ws->count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (bi == 0x7FFFFFFF) bi = 0;          // every logit NaN: token 0
   token[0] = bi;
   const int c = state[1];
@@ -1350,11 +1355,15 @@ extern "C" int bf16x_attention_decode(const uint16_t* qkv, const int32_t* pos, c
 //  - no o GEMV workgroups (four of gemv_pipe_body with the residual epilogue
 //    each, the rows and slots of bf16x_gemv_residual); they request their
 //    first rows, then wait for the attention.
-// Stages are ordered by the counters of `sync` (see sync_wait).  No workgroup
-// waits for a later one in dispatch order, and the waiting attention
-// workgroups hold at most half of the CUs, so every wait ends.  Outputs are
-// bit-identical to bf16x_gemv_prenormed, bf16x_attention_decode and
-// bf16x_gemv_residual in sequence.
+// Stages are ordered by the counters of `sync` (see sync_wait).  The
+// attention workgroups wait for the qkv workgroups, which are dispatched
+// after them: those waits end because the attention workgroups (one per CU
+// at most) hold no more than half of the device's CUs, which the launcher
+// checks against the device's CU count, so the qkv workgroups always find
+// CUs to run on.  The o workgroups, which wait for the attention, are
+// dispatched after every qkv workgroup, so they cannot keep one from
+// starting.  Outputs are bit-identical to bf16x_gemv_prenormed,
+// bf16x_attention_decode and bf16x_gemv_residual in sequence.
 constexpr int kQaSubs = 4;                      // GEMV workgroups per hardware workgroup
 constexpr int kQaThreads = 64 * kDecHWaves;     // 1024
 static_assert(kQaThreads == 256 * kQaSubs, "four 256-thread GEMV workgroups per attention-sized workgroup");
@@ -1469,11 +1478,12 @@ extern "C" int bf16x_layer_front_decode(
   if (sync_clear == sync) return BF16X_EARG;
   if (n_slots <= 0) return BF16X_EARG;
   if (n_slots > 64 * kMaxSlotsPerLane) return BF16X_ECAPACITY;
-  // the attention side: the per-query-head kernel's shapes; n_heads <= 128:
-  // the waiting attention workgroups hold at most half of the CUs
+  // the attention side: the per-query-head kernel's shapes; the waiting
+  // attention workgroups must hold at most half of this device's CUs
   if (head_dim != 128 || n_kv_heads <= 0 || n_heads <= 0 || n_heads % n_kv_heads != 0 || n_heads % 8 != 0 ||
       n_heads > 128 || max_len <= kDec1MaxLen || max_len > kDecHMaxLen)
     return BF16X_ESHAPE;
+  if (2 * n_heads > device_cus()) return BF16X_ESHAPE;
   // the GEMV side: 64 < in_f / 32 <= 128 (two 64-atom steps per wave, one
   // wave per row), out_f = the qkv rows of the attention
   if (out_f != (n_heads + 2 * n_kv_heads) * 128) return BF16X_ESHAPE;
@@ -1559,15 +1569,20 @@ extern "C" int bf16x_silu_mul(const uint16_t* gate_up, int64_t tokens, int64_t f
   return launch_status();
 }
 
+extern "C" int64_t bf16x_greedy_workspace_bytes(void) { return (int64_t)sizeof(GreedyWs); }
+
 extern "C" int bf16x_greedy(const uint16_t* logits, int64_t vocab, int64_t* token, int32_t* state, int32_t* history,
-                            int64_t history_len, bf16x_stream_t stream) {
-  if (!logits || !token || !state || (!history && history_len > 0) || history_len < 0) return BF16X_EARG;
+                            int64_t history_len, void* workspace, int64_t workspace_bytes, bf16x_stream_t stream) {
+  if (!logits || !token || !state || (!history && history_len > 0) || history_len < 0 || !workspace)
+    return BF16X_EARG;
+  if (workspace_bytes < (int64_t)sizeof(GreedyWs)) return BF16X_ECAPACITY;
+  if (!aligned16(workspace)) return BF16X_EARG;
   // greedy_kernel steps its int indices by 1024 * 8 per batch element and
   // 2 elements per batch, its ranges by a multiple of 8: the last indices
   // must not overflow
   if (vocab <= 0 || vocab > INT32_MAX - 4 * 1024 * 8 * kGreedyBlocks || history_len > INT32_MAX) return BF16X_ESHAPE;
   if (!aligned16(logits) || !aligned4(state) || ((uintptr_t)token & 7u)) return BF16X_EARG;
   hipLaunchKernelGGL(greedy_kernel, dim3(kGreedyBlocks), dim3(1024), 0, (hipStream_t)stream, logits, (int)vocab,
-                     token, state, history, (int)history_len);
+                     token, state, history, (int)history_len, (GreedyWs*)workspace);
   return launch_status();
 }

@@ -47,7 +47,7 @@ from . import _lib, ops
 
 __all__ = ["LlamaConfig", "LlamaStack", "LlamaRunner", "rope_table", "rmsnorm", "rope_kv", "attention", "pairs8_rows",
            "attention_decode", "attention_decode_supported", "attention_decode_workspace", "layer_front_decode",
-           "layer_front_supported", "layer_front_sync", "layer_front_buffers", "silu_mul", "greedy", "NORM_ADD", "NORM_STORE"]
+           "layer_front_supported", "layer_front_sync", "layer_front_buffers", "silu_mul", "greedy", "greedy_workspace", "NORM_ADD", "NORM_STORE"]
 
 NORM_ADD, NORM_STORE = 1, 2
 HEAD_DIM = 128
@@ -203,11 +203,14 @@ def attention_decode(qkv, pos, cos_sin, n_heads, n_kv_heads, k_cache, v_cache, o
     _lib.check(st, "bf16x_attention_decode")
 
 
-def layer_front_supported(n_heads, n_kv_heads, max_len, out_f, in_f) -> bool:
+def layer_front_supported(n_heads, n_kv_heads, max_len, out_f, in_f, cus=None) -> bool:
     """Shapes bf16x_layer_front_decode takes (the per-query-head attention,
-    one wave per qkv row with two 64-atom steps)."""
+    one wave per qkv row with two 64-atom steps).  cus: the device's compute
+    units, when known: the waiting attention workgroups (one per query
+    head) may hold at most half of them."""
     return (n_heads % 8 == 0 and n_heads <= 128 and n_heads % n_kv_heads == 0 and 256 < max_len <= 768
-            and in_f % 32 == 0 and 2048 < in_f <= 4096 and out_f == (n_heads + 2 * n_kv_heads) * HEAD_DIM)
+            and in_f % 32 == 0 and 2048 < in_f <= 4096 and out_f == (n_heads + 2 * n_kv_heads) * HEAD_DIM
+            and (cus is None or 2 * n_heads <= cus))
 
 
 def layer_front_sync(device, n: int = 1) -> torch.Tensor:
@@ -300,14 +303,24 @@ def silu_mul(gate_up, out, ffn, pairs8=False):
     _lib.check(st, "bf16x_silu_mul")
 
 
-def greedy(logits, token, state, history):
-    """token[0] = argmax(logits); history[state[1]] = token; state += 1."""
+def greedy_workspace(device) -> torch.Tensor:
+    """A zeroed workspace for greedy() (the launch's counter and partial
+    results); every call leaves it zeroed again."""
+    n = int(_lib.lib().bf16x_greedy_workspace_bytes())
+    return torch.zeros(-(-n // 16) * 4, dtype=torch.int32, device=device)
+
+
+def greedy(logits, token, state, history, workspace):
+    """token[0] = argmax(logits); history[state[1]] = token; state += 1.
+    workspace: greedy_workspace(); calls that share one must not overlap."""
     _bf16_dev(logits, "logits")
     _need(token.is_cuda and token.dtype == torch.int64 and token.numel() >= 1, "token: int64 GPU")
     _need(state.is_cuda and state.dtype == torch.int32 and state.numel() >= 2, "state: int32[2] GPU")
     _need(history.is_cuda and history.dtype == torch.int32, "history: int32 GPU")
+    _need(workspace.is_cuda and workspace.is_contiguous(), "workspace: greedy_workspace() on the GPU")
     st = _lib.lib().bf16x_greedy(logits.data_ptr(), logits.numel(), token.data_ptr(), state.data_ptr(),
-                                 history.data_ptr(), history.numel(), _stream(logits))
+                                 history.data_ptr(), history.numel(), workspace.data_ptr(),
+                                 workspace.numel() * workspace.element_size(), _stream(logits))
     _lib.check(st, "bf16x_greedy")
 
 
@@ -427,6 +440,7 @@ class LlamaRunner:
         self.token = torch.zeros(1, dtype=torch.int64, device=dev)
         self.state = torch.zeros(2, dtype=torch.int32, device=dev)
         self.history = torch.zeros(max(self.max_new, 1), dtype=torch.int32, device=dev)
+        self.greedy_ws = greedy_workspace(dev)
         self.zero_pos = torch.zeros(1, dtype=torch.int32, device=dev)
         self.logits = None
         self.graph = None
@@ -461,8 +475,9 @@ class LlamaRunner:
         # i + 1) uses counter buffer c(i) and zeroes its predecessor's, so consecutive launches, cyclically over
         # the step (the graph repeats it), must differ: c = 0, 1, 0, 1, ..., and 2 for the last launch
         lay0 = model.layers[0]
+        cus = torch.cuda.get_device_properties(dev).multi_processor_count
         self.front = bool(layer_front) and self.res_norm and cfg.n_layers >= 3 and layer_front_supported(
-            cfg.n_heads, cfg.n_kv_heads, self.max_len, lay0.qkv.out_features, lay0.qkv.in_features) and \
+            cfg.n_heads, cfg.n_kv_heads, self.max_len, lay0.qkv.out_features, lay0.qkv.in_features, cus) and \
             lay0.o.in_features == lay0.qkv.in_features
         if self.front:
             self.front_sync = layer_front_sync(dev, 3)
@@ -579,7 +594,7 @@ class LlamaRunner:
     def _head(self, last_down: torch.Tensor, last_res: torch.Tensor):
         rmsnorm(last_down, self.model.norm, self.normed, last_res, flags=NORM_ADD, eps=self.cfg.eps)
         self.logits = self.model.lm_head(self.normed[0])
-        greedy(self.logits, self.token, self.state, self.history)
+        greedy(self.logits, self.token, self.state, self.history, self.greedy_ws)
 
     @torch.no_grad()
     def prefill(self, ids: torch.Tensor) -> None:
@@ -607,7 +622,7 @@ class LlamaRunner:
             h = self._decode_resnorm(self.state, self.token)
             rmsnorm(h, self.model.norm, self.normed, eps=self.cfg.eps)
             self.logits = self.model.lm_head(self.normed[0])
-            greedy(self.logits, self.token, self.state, self.history)
+            greedy(self.logits, self.token, self.state, self.history, self.greedy_ws)
             return
         down = self._layers(1, self.state, self.token)
         self._head(down, self.residual[0])
@@ -629,8 +644,11 @@ class LlamaRunner:
         self.graph = g
         self._graph_logits = self.logits      # lives in the graph's pool, rewritten by every replay
 
-    def decode(self, n_steps: int, graph: bool = True) -> None:
-        """n_steps decode steps, asynchronous (no host sync)."""
+    def decode(self, n_steps: int, graph: bool = True, check: bool = True) -> None:
+        """n_steps decode steps, launched without a host sync between them.
+        check: afterwards, wait for the stream and raise if a layer launch's
+        bounded wait ran out (check_layer_launch); check=False leaves the
+        steps queued and the check to the caller."""
         if graph and self.graph is None:
             raise RuntimeError("capture() first")
         for _ in range(int(n_steps)):
@@ -639,13 +657,31 @@ class LlamaRunner:
                 self.logits = self._graph_logits
             else:
                 self.step()
+        if check:
+            self.check_layer_launch()
+
+    def check_layer_launch(self) -> None:
+        """Raise RuntimeError if any layer launch since the last check ended a
+        bounded wait by its time limit (word 1024 of its counter buffer, set by
+        the kernel and never cleared by it: sticky across launches and graph
+        replays).  The tokens and logits of those steps are then not valid.
+        The flags are cleared before raising.  Waits for the stream."""
+        if not self.front:
+            return
+        flags = self.front_sync[:, 1024]
+        if bool((flags != 0).any()):
+            flags.zero_()
+            torch.cuda.current_stream().synchronize()
+            raise RuntimeError("a layer launch (bf16x_layer_front_decode) timed out waiting for its producer "
+                               "stage: the decode steps since the last check are invalid; build the runner with "
+                               "layer_front=False to use the separate launches")
 
     def generate(self, ids: torch.Tensor, n_new: int, graph: bool = True) -> list:
         """Greedy decode of n_new tokens after the prompt; the token ids."""
         if not (1 <= n_new <= self.max_new):
             raise ValueError(f"n_new must be in [1, {self.max_new}]")
         self.prefill(ids)
-        self.decode(n_new - 1, graph=graph)
+        self.decode(n_new - 1, graph=graph)               # checks the layer launches' time-out flags
         return self.history[:n_new].tolist()
 
     def kv_bytes_per_step(self) -> int:

@@ -31,7 +31,13 @@
  *    default stream) and is asynchronous.
  *  - Return value: 0 = success, < 0 = invalid argument (see BF16X_E*),
  *    > 0 = a hipError_t reported by the runtime.
- *  - Entry points are stateless and reentrant.
+ *  - Entry points keep no state between calls, and concurrent calls on
+ *    different streams are safe when their output and workspace buffers
+ *    differ, with one exception: bf16x_gguf_gemv_noalloc stages x in one
+ *    fixed array per device, so its calls on one device must not overlap.
+ *    Calls that share a workspace or counter buffer (bf16x_greedy's
+ *    workspace, bf16x_layer_front_decode's sync buffers) must not overlap
+ *    either.  bf16x_set_tuning changes kernel choices for the whole process.
  */
 #ifndef BF16X_HIP_H
 #define BF16X_HIP_H
@@ -325,8 +331,7 @@ enum {
   BF16X_TUNE_GEMM_WS_GROUPED = 16, /* 0: the wave-specialised GEMM in one-step (64-column) tiles   */
   BF16X_TUNE_GEMM_WS_RESIDENT = 17,/* resident blocks the wave-specialised GEMM plans its rounds for */
   BF16X_TUNE_ATTN_MFMA = 18,       /* prefill attention: 0 the scalar kernel, 1 the MFMA kernel       */
-  BF16X_TUNE_GEMM_WS5_MIN_ROWS = 19,/* smallest M of the one-wave-per-SIMD GEMM (default 0: never) */
-  BF16X_TUNE_COUNT = 20
+  BF16X_TUNE_COUNT = 19
 };
 int bf16x_set_tuning(int32_t key, int64_t value);
 /* Current value of a key (-1 = automatic; also returned for an unknown key). */

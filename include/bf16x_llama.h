@@ -186,13 +186,18 @@ int bf16x_layer_front_decode(const void* h, const uint16_t* norm_weight, float e
                              const uint8_t* o_tile_sat, int64_t o_out_f, uint16_t* o_y, void* sync,
                              void* sync_clear, int64_t sync_bytes, bf16x_stream_t stream);
 
+/* Bytes of bf16x_greedy's workspace. */
+int64_t bf16x_greedy_workspace_bytes(void);
+
 /* Greedy step: token[0] = argmax(logits[0 .. vocab)) (the first maximum),
  * history[state[1]] = token[0] when state[1] < history_len, then state[1]++
  * and state[0]++.  logits 16-byte aligned.  The launch's workgroups meet in
- * one device-wide set of partial results: calls on one device must not
+ * `workspace` (bf16x_greedy_workspace_bytes, 16-byte aligned, zeroed once by
+ * the caller before its first use; every call leaves it zeroed again): calls
+ * with different workspaces are independent, calls sharing one must not
  * overlap (stream order, one graph replay at a time). */
 int bf16x_greedy(const uint16_t* logits, int64_t vocab, int64_t* token, int32_t* state, int32_t* history,
-                 int64_t history_len, bf16x_stream_t stream);
+                 int64_t history_len, void* workspace, int64_t workspace_bytes, bf16x_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -253,8 +253,10 @@ def rel_err(y: np.ndarray, y_ref: np.ndarray, floor_frac: float = 1e-3):
 def bench_weight_bits(out_f: int, in_f: int, seed: int = 0) -> np.ndarray:
     """N(0, 0.02) with 1 % of entries scaled x30, rounded to bf16 (RNE).
 
-    numpy-only restatement of the configuration's weight recipe; the tests
-    and the benchmark draw the device copy with the same generator."""
+    numpy restatement of the configuration's weight distribution, drawn
+    with numpy's default_rng: the same distribution as the benchmark's
+    weights (bench.bench_weight, torch's CPU generator) but not the same
+    values.  The full-size GPU tests use bench.bench_weight itself."""
     rng = np.random.default_rng(seed)
     w = (rng.standard_normal((out_f, in_f), dtype=np.float32) * np.float32(0.02))
     n = w.size

@@ -197,55 +197,6 @@ def test_gemm_ws_groups_and_splits(bx, tune, grouped, split, M, out_f, in_f):
     assert not np.any(got[flush] & 0x7FFF)
 
 
-# The one-wave-per-SIMD kernel (512-token tiles, four-step groups; the default
-# from 448 rows), forced from one row: partial tiles (waves with no tokens),
-# ragged out_f, K splits forced to 1 and 3, the mixed round plan, exact and
-# saturated, and the decoded weight bit for bit through identity rows.
-@pytest.mark.parametrize("split", [-1, 1, 3])
-@pytest.mark.parametrize("M,out_f,in_f", [(300, 300, 4096), (700, 136, 1024), (260, 256, 3072), (64, 130, 2048)])
-def test_gemm_ws5(bx, tune, split, M, out_f, in_f):
-    print("gemm ws5", M, out_f, in_f, "split", split, flush=True)
-    tune(gemm_ws5_min_rows=1, gemm_ws_split=split)
-    bits = dc.bench_weight_bits(out_f, in_f, seed=out_f + split + 5)
-    d = bx.bf16x_quantize(bits_tensor(bits))
-    g = to_dev(d)
-    dn = _np(d)
-    plan = bx.build_plan_host(d, device=DEV)
-    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M + split + 5)).to(torch.bfloat16)
-    for p, sat in ((plan, False), (None, True)):
-        y = bx.bf16x_gemm(x.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
-                          plan=p, path="fused")
-        check_tol(y.float().cpu().numpy(), dc.gemm_ref(dn, x.float().numpy(), saturated=sat))
-    eye = torch.zeros(M, in_f, dtype=torch.bfloat16)
-    cols = (torch.arange(M) * (in_f // M)) % in_f if M <= in_f else torch.arange(M) % in_f
-    eye[torch.arange(M), cols] = 1
-    w_cols = bx.bf16x_gemm(eye.to(DEV), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
-                           plan=plan, path="fused")
-    got = w_cols.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
-    want = bits[:, cols.numpy()].T
-    flush = (want & 0x7F80) == 0
-    assert np.array_equal(np.where(flush, 0, got), np.where(flush, 0, want))
-
-
-@pytest.mark.parametrize("resident", [4, 5])
-def test_gemm_ws5_mixed_rounds(bx, tune, resident):
-    """1100 rows x 300 columns at 512-token tiles: 3 M tiles x 3 W tiles, with
-    4 or 5 resident blocks run as whole tiles plus split last-round tiles."""
-    M, out_f, in_f = 1100, 300, 1024
-    tune(gemm_ws5_min_rows=1, gemm_ws_resident=resident)
-    bits = dc.bench_weight_bits(out_f, in_f, seed=resident + 11)
-    d = bx.bf16x_quantize(bits_tensor(bits))
-    g = to_dev(d)
-    dn = _np(d)
-    plan = bx.build_plan_host(d, device=DEV)
-    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(resident + 11)).to(torch.bfloat16)
-    for p, sat in ((plan, False), (None, True)):
-        for dt in (torch.bfloat16, torch.float32):
-            y = bx.bf16x_gemm(x.to(DEV).to(dt), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"],
-                              out_f, in_f, plan=p, path="fused")
-            check_tol(y.float().cpu().numpy(), dc.gemm_ref(dn, x.float().numpy(), saturated=sat))
-
-
 # Whole-K tiles in full rounds, then the last round's tiles split over K: with
 # the resident block count forced to 4 or 5, the 6 tiles of 300 x 300 run as
 # 4 whole tiles + 2 tiles x 2 K ranges, or 5 whole tiles + 1 tile x 5 ranges

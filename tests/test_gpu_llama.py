@@ -352,19 +352,46 @@ def test_gemv_swiglu_matches_unfused(bx, F, in_f, mode):
 
 
 @torch.no_grad()
-@pytest.mark.parametrize("V", [1000, 1003, 128256, 140003])
+@pytest.mark.parametrize("V", [3, 100, 1000, 1003, 128256, 140003])
 def test_greedy(bx, V):
+    """V < 256: most of the 32 workgroups have an empty range."""
     logits = rnd(V, 12)
     logits[V // 3] = 9.0
     logits[V - 1] = 9.0                                  # tie: the first index wins
     tok = torch.zeros(1, dtype=torch.int64, device=DEV)
     state = torch.tensor([50, 0], dtype=torch.int32, device=DEV)
     hist = torch.full((2,), -1, dtype=torch.int32, device=DEV)
+    ws = llama.greedy_workspace(DEV)
     lg = logits.to(DEV)
     for _ in range(3):                                   # the third call is past the history: not written
-        llama.greedy(lg, tok, state, hist)
+        llama.greedy(lg, tok, state, hist, ws)
     assert int(tok) == V // 3 == int(torch.argmax(logits.float()))
     assert hist.tolist() == [V // 3, V // 3] and state.tolist() == [53, 3]
+    assert not ws.any()                                  # the counter is back at zero
+
+
+@torch.no_grad()
+def test_greedy_two_streams(bx):
+    """Two greedy launches in flight at once on two streams, each with its
+    own workspace, give each its own argmax."""
+    V = 128256
+    la, lb = rnd(V, 21).to(DEV), rnd(V, 22).to(DEV)
+    la[7], lb[V - 9] = 11.0, 11.0
+    outs = []
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    args = []
+    for lg in (la, lb):
+        args.append((lg, torch.zeros(1, dtype=torch.int64, device=DEV), torch.zeros(2, dtype=torch.int32, device=DEV),
+                     torch.zeros(200, dtype=torch.int32, device=DEV), llama.greedy_workspace(DEV)))
+    torch.cuda.synchronize()
+    for _ in range(100):
+        with torch.cuda.stream(sa):
+            llama.greedy(*args[0])
+        with torch.cuda.stream(sb):
+            llama.greedy(*args[1])
+    torch.cuda.synchronize()
+    assert args[0][3][:100].tolist() == [7] * 100
+    assert args[1][3][:100].tolist() == [V - 9] * 100
 
 
 @torch.no_grad()
@@ -588,6 +615,13 @@ def test_layer_front_decode_step(bx):
         assert ra.generate(ids, 10, graph=True) == ta, rep
         assert torch.equal(ra.logits, la), rep
         assert not ra.front_sync[:, 1024].any()
+    # a timed-out wait (its flag, set here from the host) makes the runner raise
+    # and clears the flag
+    ra.front_sync[1, 1024] = 1
+    with pytest.raises(RuntimeError, match="timed out"):
+        ra.generate(ids, 10, graph=True)
+    assert not ra.front_sync[:, 1024].any()
+    assert ra.generate(ids, 10, graph=True) == ta
 
 
 @torch.no_grad()

@@ -96,11 +96,16 @@ def test_entry_points_validate_before_launch():
     assert _call("bf16x_gemv_norm", *norm_args(p, q, q, q, 0)) == _lib.EARG
     assert _call("bf16x_gemv_norm", *norm_args(p, q, q, p, 0)) == _lib.EARG
     # greedy: misaligned token, history without length
-    assert _call("bf16x_greedy", p, 8, p + 4, p, p, 1, None) == _lib.EARG
-    assert _call("bf16x_greedy", p, 8, p, p, None, 1, None) == _lib.EARG
-    assert _call("bf16x_greedy", p, 0, p, p, p, 1, None) == _lib.ESHAPE
+    gw = int(_lib.lib().bf16x_greedy_workspace_bytes())
+    assert _call("bf16x_greedy", p, 8, p + 4, p, p, 1, p, gw, None) == _lib.EARG
+    assert _call("bf16x_greedy", p, 8, p, p, None, 1, p, gw, None) == _lib.EARG
+    assert _call("bf16x_greedy", p, 0, p, p, p, 1, p, gw, None) == _lib.ESHAPE
+    # workspace: missing, too small, misaligned
+    assert _call("bf16x_greedy", p, 8, p, p, p, 1, None, gw, None) == _lib.EARG
+    assert _call("bf16x_greedy", p, 8, p, p, p, 1, p, gw - 1, None) == _lib.ECAPACITY
+    assert _call("bf16x_greedy", p, 8, p, p, p, 1, p + 4, gw, None) == _lib.EARG
     # a vocabulary whose last index batch would overflow the kernel's int indices
-    assert _call("bf16x_greedy", p, 2 ** 31 - 1 - 2 * 1024 * 8 * 16 + 1, p, p, p, 1, None) == _lib.ESHAPE
+    assert _call("bf16x_greedy", p, 2 ** 31 - 1 - 2 * 1024 * 8 * 16 + 1, p, p, p, 1, p, gw, None) == _lib.ESHAPE
     # zero rows / tokens: nothing to launch
     assert _call("bf16x_rmsnorm", p, None, 0, None, p, p, 0, 64, 1e-5, 0, None) == _lib.OK
     assert _call("bf16x_silu_mul", p, 0, 16, 1, p, None) == _lib.OK
