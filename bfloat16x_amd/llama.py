@@ -305,7 +305,7 @@ def silu_mul(gate_up, out, ffn, pairs8=False):
 
 def greedy_workspace(device) -> torch.Tensor:
     """A zeroed workspace for greedy() (the launch's counter and partial
-    results); every call leaves it zeroed again."""
+    results); every call puts the counter, word 0, back to zero."""
     n = int(_lib.lib().bf16x_greedy_workspace_bytes())
     return torch.zeros(-(-n // 16) * 4, dtype=torch.int32, device=device)
 

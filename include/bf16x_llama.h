@@ -193,7 +193,8 @@ int64_t bf16x_greedy_workspace_bytes(void);
  * history[state[1]] = token[0] when state[1] < history_len, then state[1]++
  * and state[0]++.  logits 16-byte aligned.  The launch's workgroups meet in
  * `workspace` (bf16x_greedy_workspace_bytes, 16-byte aligned, zeroed once by
- * the caller before its first use; every call leaves it zeroed again): calls
+ * the caller before its first use; every call puts its counter, the first
+ * word, back to zero): calls
  * with different workspaces are independent, calls sharing one must not
  * overlap (stream order, one graph replay at a time). */
 int bf16x_greedy(const uint16_t* logits, int64_t vocab, int64_t* token, int32_t* state, int32_t* history,

@@ -367,7 +367,7 @@ def test_greedy(bx, V):
         llama.greedy(lg, tok, state, hist, ws)
     assert int(tok) == V // 3 == int(torch.argmax(logits.float()))
     assert hist.tolist() == [V // 3, V // 3] and state.tolist() == [53, 3]
-    assert not ws.any()                                  # the counter is back at zero
+    assert int(ws[0]) == 0                               # the counter is back at zero
 
 
 @torch.no_grad()
