@@ -93,7 +93,8 @@ def time_launches(fn, n_launch: int, warmup: int, stream, queued: bool = False) 
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     if queued:
-        torch.cuda._sleep(20_000_000)
+        # long enough for the host to enqueue every launch (~20 us of host time each)
+        torch.cuda._sleep(max(20_000_000, 50_000 * n_launch))
     t0.record(stream)
     for i in range(n_launch):
         fn(i)
@@ -611,7 +612,7 @@ def main():
     def step_bf16(i):
         torch.nn.functional.linear(xb, wcopies[i % len(wcopies)])
 
-    sec_bf16 = time_launches(step_bf16, max(200, args.steps // 4), 20, stream)
+    sec_bf16 = time_launches(step_bf16, max(200, args.steps // 4), 20, stream, queued=True)
     log(f"bf16 F.linear gemv: {sec_bf16 * 1e6:.2f} us ({wd.numel() * 2 / sec_bf16 / 1e9:.1f} GB/s of bf16 bytes)")
 
     # ---- device encoder at the headline shape (bf16 weight in HBM -> dict)
