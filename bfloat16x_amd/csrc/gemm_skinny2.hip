@@ -362,14 +362,31 @@ __global__ __launch_bounds__(256 * KQ) void gemm_skinny2_kernel(
   }
 }
 
-template <bool YF32>
+// y = the sum of the K splits' fp32 partials in split order; four
+// consecutive elements per thread (16-byte loads) where count % 4 == 0
+template <bool YF32, bool VEC>
 __global__ __launch_bounds__(256) void skinny2_reduce_kernel(const float* __restrict__ ws, int64_t count, int nsplit,
                                                              void* __restrict__ y) {
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
-    float s = ws[i];
-    for (int k = 1; k < nsplit; ++k) s += ws[(int64_t)k * count + i];
-    if constexpr (YF32) ((float*)y)[i] = s;
-    else ((uint16_t*)y)[i] = (uint16_t)f32_to_bf16_rne(s);
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  if constexpr (VEC) {
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < count; i += (int64_t)gridDim.x * 256 * 4) {
+      f32x4v s = *(const f32x4v*)(ws + i);
+      for (int k = 1; k < nsplit; ++k) s += *(const f32x4v*)(ws + (int64_t)k * count + i);
+      if constexpr (YF32) {
+        *(f32x4v*)((float*)y + i) = s;
+      } else {
+        const float v0 = s.x, v1 = s.y, v2 = s.z, v3 = s.w;
+        *(u32x2a*)((uint16_t*)y + i) = u32x2a{f32_to_bf16_rne(v0) | (f32_to_bf16_rne(v1) << 16),
+                                              f32_to_bf16_rne(v2) | (f32_to_bf16_rne(v3) << 16)};
+      }
+    }
+  } else {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+      float s = ws[i];
+      for (int k = 1; k < nsplit; ++k) s += ws[(int64_t)k * count + i];
+      if constexpr (YF32) ((float*)y)[i] = s;
+      else ((uint16_t*)y)[i] = (uint16_t)f32_to_bf16_rne(s);
+    }
   }
 }
 
@@ -509,13 +526,14 @@ int bf16x_gemm_skinny2_launch(const uint16_t* x, int64_t M, const uint32_t* s, c
 #undef BF16X_S2
   if (partial) {
     const int64_t count = M * out_f;
-    const int64_t blocks = std::min<int64_t>((count + 255) / 256, 4096);
-    if (yf32)
-      hipLaunchKernelGGL(skinny2_reduce_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)part,
-                         count, sp.ks, y);
-    else
-      hipLaunchKernelGGL(skinny2_reduce_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)part,
-                         count, sp.ks, y);
+    const bool vec = count % 4 == 0 && aligned16(workspace) && aligned16(y);
+    const int64_t blocks = std::min<int64_t>(((vec ? count / 4 : count) + 255) / 256, 4096);
+#define BF16X_S2R(YF_, VEC_)                                                                                 \
+  hipLaunchKernelGGL((skinny2_reduce_kernel<YF_, VEC_>), dim3((unsigned)blocks), dim3(256), 0, st, (const float*)part, \
+                     count, sp.ks, y)
+    if (yf32) { if (vec) BF16X_S2R(true, true); else BF16X_S2R(true, false); }
+    else { if (vec) BF16X_S2R(false, true); else BF16X_S2R(false, false); }
+#undef BF16X_S2R
   }
   return BF16X_OK;
 }

@@ -810,19 +810,38 @@ __global__ __launch_bounds__(256) void x_op_kernel(const uint16_t* __restrict__ 
 // of the split tiles' 256 x 128 partials, in order.
 template <bool YF32>
 __global__ __launch_bounds__(256) void ws_tile_reduce_kernel(const float* __restrict__ part, WsGrid g, int nsplit,
-                                                             int64_t M, int64_t out_f, void* __restrict__ y) {
+                                                             int64_t M, int64_t out_f, void* __restrict__ y,
+                                                             bool yal) {
+  // four consecutive columns of one tile row per thread (kBN % 4 == 0): 16-byte
+  // partial loads, an 8-byte (bf16) or 16-byte (fp32) store when the row's
+  // four outputs are in range and aligned (yal: y is 16-byte aligned)
   const int64_t tsz = (int64_t)g.bm * kBN;
   const int64_t count = (int64_t)g.ltiles * tsz;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < count; i += (int64_t)gridDim.x * 256) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < count; i += (int64_t)gridDim.x * 256 * 4) {
     const int lt = (int)(i / tsz), e = (int)(i % tsz);
     const int tile = g.full + lt;
     const int64_t row = (int64_t)(tile % g.mtiles) * g.bm + e / kBN;
     const int64_t col = (int64_t)(tile / g.mtiles) * kBN + e % kBN;
     if (row >= M || col >= out_f) continue;
-    float s = part[i];
-    for (int k = 1; k < nsplit; ++k) s += part[(int64_t)k * count + i];
-    if constexpr (YF32) ((float*)y)[row * out_f + col] = s;
-    else ((uint16_t*)y)[row * out_f + col] = (uint16_t)f32_to_bf16_rne(s);
+    f32x4v s = *(const f32x4v*)(part + i);
+    for (int k = 1; k < nsplit; ++k) s += *(const f32x4v*)(part + (int64_t)k * count + i);
+    const float v[4] = {s.x, s.y, s.z, s.w};
+    const int64_t o = row * out_f + col;
+    if (yal && col + 3 < out_f && (o & 3) == 0) {
+      if constexpr (YF32) {
+        *(f32x4v*)((float*)y + o) = s;
+      } else {
+        const uint32_t lo = f32_to_bf16_rne(v[0]) | (f32_to_bf16_rne(v[1]) << 16);
+        const uint32_t hi = f32_to_bf16_rne(v[2]) | (f32_to_bf16_rne(v[3]) << 16);
+        *(u32x2a*)((uint16_t*)y + o) = u32x2a{lo, hi};
+      }
+    } else {
+      for (int c = 0; c < 4 && col + c < out_f; ++c) {
+        if constexpr (YF32) ((float*)y)[o + c] = v[c];
+        else ((uint16_t*)y)[o + c] = (uint16_t)f32_to_bf16_rne(v[c]);
+      }
+    }
   }
 }
 
@@ -948,13 +967,13 @@ int bf16x_gemm_ws_launch(const uint16_t* x, int64_t M, const uint32_t* s, const 
 #undef BF16X_WS1
   if (w.nsplit > 1) {
     const int64_t count = (int64_t)w.g.ltiles * ((int64_t)w.g.bm * kBN);
-    const int64_t blocks_r = std::min<int64_t>((count + 255) / 256, 4096);
+    const int64_t blocks_r = std::min<int64_t>((count / 4 + 255) / 256, 4096);
     if (yf32)
       hipLaunchKernelGGL(ws_tile_reduce_kernel<true>, dim3((unsigned)blocks_r), dim3(256), 0, st,
-                         (const float*)part, w.g, w.nsplit, M, out_f, y);
+                         (const float*)part, w.g, w.nsplit, M, out_f, y, aligned16(y));
     else
       hipLaunchKernelGGL(ws_tile_reduce_kernel<false>, dim3((unsigned)blocks_r), dim3(256), 0, st,
-                         (const float*)part, w.g, w.nsplit, M, out_f, y);
+                         (const float*)part, w.g, w.nsplit, M, out_f, y, aligned16(y));
   }
   return launch_status();
 }
