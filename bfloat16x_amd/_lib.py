@@ -47,6 +47,8 @@ PROTOTYPES = {
     "bf16x_gemm_workspace": (_c_i64, [_c_i64, _c_i64, _c_i64]),
     "bf16x_gemm": (ctypes.c_int, [_P, _c_i32, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _P,
                                   _c_i64, _c_i64, _c_i32, _c_i32, _P, _c_i32, _P, _c_i64, _P]),
+    "bf16x_gemm_rows": (ctypes.c_int, [_P, _c_i32, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P,
+                                       _P, _c_i64, _c_i64, _c_i32, _c_i32, _P, _c_i32, _P]),
     "bf16x_fp32_to_bf16_host": (ctypes.c_int, [_P, _c_i64, _P, _c_i32]),
     "bf16x_gguf_quantize_host": (ctypes.c_int, [_P, _c_i64, _P, _c_i32]),
     "bf16x_gguf_decode": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i64, _P, _c_i32, _P]),

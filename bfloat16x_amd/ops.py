@@ -307,10 +307,24 @@ def bf16x_fused_gemv(x, sign, mant, delta, emax, olk, old, oloff, out_f, in_f, g
     return bf16x_gemv(x, sign, mant, delta, emax, out_f, in_f, plan=plan)
 
 
+# Activation rows up to which bf16x_gemm runs the row-streaming few-row
+# kernel (bf16x_gemm_rows in the C ABI: weights of 2048 or 4096 columns).
+GEMM_ROWS_MAX = 16
+GEMM_ROWS_IN_F = (2048, 4096)
+
+
 def _gemm_launch(x2, s, m, d, e, out_f, in_f, plan, y, y_dtype, sub=16):
     mode = _lib.SATURATED if plan is None else _lib.EXACT
-    kp_off, kp_ent = plan.kplan() if plan is not None else (None, None)
     L = _lib.lib()
+    if x2.shape[0] <= GEMM_ROWS_MAX and in_f in GEMM_ROWS_IN_F:
+        st = L.bf16x_gemm_rows(x2.data_ptr(), _lib.BF16, x2.shape[0], s.data_ptr(), s.numel(), m.data_ptr(),
+                               m.numel(), d.data_ptr(), d.numel(), e.data_ptr(), e.numel(),
+                               _lib.ptr(plan.tile_off) if plan is not None else None,
+                               _lib.ptr(plan.tile_ent) if plan is not None else None, out_f, in_f, int(sub),
+                               mode, y.data_ptr(), y_dtype, _lib.stream_of(s.device))
+        _lib.check(st, "bf16x_gemm_rows")
+        return
+    kp_off, kp_ent = plan.kplan() if plan is not None else (None, None)
     ws_bytes = int(L.bf16x_gemm_workspace(x2.shape[0], out_f, in_f))
     ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=x2.device) if ws_bytes else None
     st = L.bf16x_gemm(x2.data_ptr(), _lib.BF16, x2.shape[0], s.data_ptr(), s.numel(), m.data_ptr(),

@@ -200,6 +200,23 @@ int bf16x_gemm(const void* x, int32_t x_dtype, int64_t M,
                void* y, int32_t y_dtype, void* workspace, int64_t workspace_bytes,
                bf16x_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Fused decode + GEMM for few activation rows, the same product as
+ * bf16x_gemm at the reference's smallest block (bf16x_gemm_fused.py:97-114,
+ * BM = 16): y[M, out_f] = x[M, in_f] . W^T, fp32 accumulation, for
+ * 1 <= M <= 16 and in_f 2048 or 4096.  Each weight row is read once, in the
+ * GEMV's pattern, with the ROW plan (tile_off, tile_ent of bf16x_plan_host /
+ * bf16x_plan_from_csr) for EXACT; no workspace.  x: dev bf16 [M, in_f],
+ * y: dev [M, out_f] of y_dtype (BF16X_BF16 or BF16X_F32), both 4-byte
+ * aligned.  Other M or in_f return BF16X_ESHAPE.  All pointers dev.
+ * ------------------------------------------------------------------------ */
+int bf16x_gemm_rows(const void* x, int32_t x_dtype, int64_t M,
+                    const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                    const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                    const uint32_t* tile_off, const uint32_t* tile_ent,
+                    int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
+                    void* y, int32_t y_dtype, bf16x_stream_t stream);
+
 /* ========================================================================
  * GGUF half-block variant (bf16x_gguf_block.py, GGML_TYPE_BF16X): blocks of
  * 32 row-major weights, 46 bytes = [emax[2] | sign[4] | mant[28] |

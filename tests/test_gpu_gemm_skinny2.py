@@ -26,6 +26,13 @@ def bx():
     return m
 
 
+@pytest.fixture(autouse=True)
+def _no_row_kernel(bx, monkeypatch):
+    """bf16x_gemm runs the row-streaming kernel for M <= 16 at in_f 2048 /
+    4096 (test_gpu_gemm_rows.py); these tests pin the 16x16x32 kernel."""
+    monkeypatch.setattr(bx.ops, "GEMM_ROWS_MAX", 0)
+
+
 def _np(d):
     return {k: (v.numpy() if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
 
