@@ -104,8 +104,11 @@ def time_launches(fn, n_launch: int, warmup: int, stream, queued: bool = False) 
 
 
 def gemm_kernel_name(M: int, out_f: int, in_f: int) -> str:
-    """The kernel the fused GEMM path runs for M rows (bf16x_gemm's default
-    dispatch in the C ABI)."""
+    """The kernel the fused GEMM path runs for M rows (bfloat16x_amd.bf16x_gemm's
+    default dispatch: bf16x_gemm_rows, else bf16x_gemm in the C ABI)."""
+    from bfloat16x_amd import ops
+    if M <= ops.GEMM_ROWS_MAX and in_f in ops.GEMM_ROWS_IN_F:
+        return "gemm_rows_kernel (rows streamed as in the GEMV, 16x16x32 MFMA)"
     if M <= 64 and in_f % 128 == 0:
         return "gemm_skinny2_kernel (16x16x32 MFMA, few rows)"
     if M <= 32:
