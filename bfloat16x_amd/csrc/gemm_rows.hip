@@ -56,11 +56,12 @@ constexpr int kRedBytes = kWaves * 64 * 16;   // partial sums: per wave 64 lanes
 constexpr int kEntBatches = 2;                // plan entries prefetched per lane per row (64 per batch)
 constexpr int kMaxRowsWG = 120;               // rows per workgroup at most (its plan offsets in 2 registers)
 
-// 16-byte chunk k (0..3) of atom a in an LDS tile row, swizzled by a / 4:
-// the 16 lanes of a decode write (16 consecutive atoms, same k) then cover
-// all 64 banks.  An MFMA read (16 rows x 4 atoms, same chunk) starts row r,
-// atom q at bank 4 (r + 4 q) mod 64 with the 16-byte row skew: every 4-bank
-// group is hit exactly 4 times, the minimum for 64 distinct 16-byte reads.
+// 16-byte chunk k (0..3) of atom a in an LDS tile row, swizzled by a / 4,
+// rows skewed by 16 bytes, so that the lanes of a decode write (consecutive
+// atoms, same k) and of an MFMA read (16 rows x 4 atoms, same chunk) spread
+// over the banks.  The counters still report about two conflict cycles per
+// LDS instruction cycle; other swizzles (by a / 2) and skews (32 bytes)
+// measured within 1 % of this one.
 __device__ __forceinline__ int chunk_off(int a, int k) { return a * 64 + ((k ^ (a >> 2)) & 3) * 16; }
 
 // Workgroup b takes rows [b R, min((b + 1) R, out_f)), R = rows_per_wg (a
