@@ -50,8 +50,6 @@ constexpr int kRPW = 2;                       // rows of a group per wave
 constexpr int kWaves = kGroupRows / kRPW;     // waves per workgroup
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxTokens = 16;
-constexpr int kRowBytes = 128 * 64 + 16;      // LDS tile row: 128 atoms x 64 bytes + 16 (bank skew)
-constexpr int kTileBytes = kGroupRows * kRowBytes;
 constexpr int kRedBytes = kWaves * 64 * 16;   // partial sums: per wave 64 lanes x 4 floats
 constexpr int kEntBatches = 2;                // plan entries prefetched per lane per row (64 per batch)
 constexpr int kMaxRowsWG = 120;               // rows per workgroup at most (its plan offsets in 2 registers)
@@ -76,11 +74,13 @@ __global__ __launch_bounds__(kThreads) void gemm_rows_kernel(const uint16_t* __r
                                                          const uint32_t* __restrict__ tile_ent, int out_f, int in_f,
                                                          int rows_per_wg, void* __restrict__ y) {
   constexpr int P = 64 * NA;                  // atoms per row
+  constexpr int kRowBytes = P * 64 + 16;      // LDS tile row: P atoms x 64 bytes + 16 (bank skew)
+  constexpr int kTileBytes = kGroupRows * kRowBytes;
   constexpr int S = P / 4;                    // MFMA k-steps per row (128 columns each)
   constexpr int SW = S / kWaves;              // k-steps per wave
   static_assert(SW >= 1 && S % kWaves == 0, "whole k-steps per wave");
   // decoded tile, partial sums, a slot per lane for masked plan writes
-  // (139,776 bytes with 8 waves)
+  // (139,776 bytes at 4096 columns, 74,240 at 2048)
   __shared__ __attribute__((aligned(16))) uint8_t lds[kTileBytes + kRedBytes + 256];
   uint8_t* const tile = lds;
   float* const red = (float*)(lds + kTileBytes);
