@@ -162,6 +162,20 @@ def test_gpu_entry_points_validate_before_launch():
                           None) == _lib.ESHAPE
     assert lib.bf16x_gemv(fake, 0, fake, ws, fake, wm, fake, wd, fake, ne, None, None, None, 0, 64, 16, 1, fake,
                           None) == _lib.ESHAPE
+    # row-streaming GEMM: M in 1..16, in_f 2048 or 4096, bf16 x, a row plan in exact mode
+    n3 = 32 * 2048
+    w3 = (dc.stream_words(n3, 1), dc.stream_words(n3, 7), dc.stream_words(n3, 3), n3 // 16)
+
+    def rows(M=4, x_dtype=0, y_dtype=0, mode=1, plan=(None, None), in_f=2048, w=w3):
+        return lib.bf16x_gemm_rows(fake, x_dtype, M, fake, w[0], fake, w[1], fake, w[2], fake, w[3], plan[0], plan[1],
+                                   32, in_f, 16, mode, fake, y_dtype, None)
+    assert rows(M=0) == _lib.ESHAPE and rows(M=17) == _lib.ESHAPE
+    n4 = 32 * 1024
+    assert rows(in_f=1024, w=(dc.stream_words(n4, 1), dc.stream_words(n4, 7), dc.stream_words(n4, 3),
+                              n4 // 16)) == _lib.ESHAPE
+    assert rows(x_dtype=2) == _lib.EDTYPE and rows(y_dtype=1) == _lib.EDTYPE
+    assert rows(mode=0) == _lib.EARG                                   # exact mode without a plan
+    assert rows(w=(w3[0], w3[1] - 1, w3[2], w3[3])) == _lib.ESTREAM_LEN
     # the layer launch (qkv projection + decode attention + o projection):
     # out_f must be the qkv rows of the heads, in_f in (2048, 4096], max_len
     # in (256, 768], sync large enough and not its own clear buffer
