@@ -191,3 +191,18 @@ def test_rows_full_size(bx, M, out_f, in_f):
     y = _rows(bx, x, g, out_f, in_f, plan)
     mx, med = check_tol(y.float().cpu().numpy(), y_ref)
     print("rows full-size rel err max %.2e median %.2e" % (mx, med), flush=True)
+
+
+@pytest.mark.parametrize("lead", [(1,), (1, 1)])
+def test_one_row_runs_the_gemv(bx, lead):
+    """bf16x_gemm with one bf16 row returns the GEMV's output bit for bit (the
+    dispatch sends it there), in the input's leading shape."""
+    out_f, in_f = 1000, 4096
+    bits, d, g, plan = _weight(bx, out_f, in_f, seed=31)
+    x = torch.randn(*lead, in_f, generator=torch.Generator().manual_seed(31)).to(torch.bfloat16).to(DEV)
+    for p in (plan, None):
+        y = bx.bf16x_gemm(x, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f, plan=p)
+        yv = bx.bf16x_gemv(x.reshape(-1), g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f,
+                           in_f, plan=p)
+        assert y.shape == (*lead, out_f) and y.dtype == torch.bfloat16
+        assert torch.equal(y.reshape(-1).view(torch.int16), yv.view(torch.int16))

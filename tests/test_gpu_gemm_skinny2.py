@@ -29,8 +29,10 @@ def bx():
 @pytest.fixture(autouse=True)
 def _no_row_kernel(bx, monkeypatch):
     """bf16x_gemm runs the row-streaming kernel for M <= 16 at in_f 2048 /
-    4096 (test_gpu_gemm_rows.py); these tests pin the 16x16x32 kernel."""
+    4096 (test_gpu_gemm_rows.py) and the GEMV for one bf16 row; these tests
+    pin the 16x16x32 kernel."""
     monkeypatch.setattr(bx.ops, "GEMM_ROWS_MAX", 0)
+    monkeypatch.setattr(bx.ops, "GEMM_ONE_ROW_GEMV", False)
 
 
 def _np(d):
