@@ -45,6 +45,30 @@ __device__ __forceinline__ void load_x_atom(const void* __restrict__ x, int64_t 
   }
 }
 
+// bf16 x values of atom a as loaded (natural order: word k = elements 2k,
+// 2k + 1), for a caller that puts them in pair order later (to_pair_order):
+// the loads can then be issued ahead of others without waiting for them.
+__device__ __forceinline__ void load_x_raw(const void* __restrict__ x, int64_t a, uint32_t* xr) {
+  const u32x4a* xb = (const u32x4a*)((const uint16_t*)x + 32 * a);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const u32x4a v = xb[c];
+    xr[4 * c] = v.x; xr[4 * c + 1] = v.y; xr[4 * c + 2] = v.z; xr[4 * c + 3] = v.w;
+  }
+}
+
+// Natural -> pair order in place (word j = element j | element j + 16 << 16).
+__device__ __forceinline__ void to_pair_order(uint32_t* xr) {
+  uint32_t t[16];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    t[2 * k] = perm(xr[8 + k], xr[k], 0x05040100u);
+    t[2 * k + 1] = perm(xr[8 + k], xr[k], 0x07060302u);
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) xr[k] = t[k];
+}
+
 // Dot of an atom's 16 decoded pair words with bf16 x in pair order.
 __device__ __forceinline__ void dot_pairs_bf16(const uint32_t* w, const uint32_t* xr, float& acc0, float& acc1) {
 #pragma unroll
@@ -303,7 +327,12 @@ __device__ __forceinline__ void gemv_pipe_body(
   // prologue, in the order the first row needs its data (vector loads
   // complete in issue order, so a wait for a load also waits for every load
   // issued before it): row offsets, this thread's x values, the row's atoms,
-  // then the entries (which need the offsets)
+  // then the entries (which need the offsets).  bf16 x that this kernel
+  // stages from memory is loaded as raw words by the threads that store it
+  // and put in pair order at the LDS store, so the store waits for x alone,
+  // not for the row's atoms behind it (the permutation next to the loads
+  // made the compiler issue them after the atoms, or wait for them before
+  // issuing the atoms)
   if constexpr (EXACT) {
     load_off(r, eb, ee);
     load_off(rn, ebn, een);
@@ -345,8 +374,13 @@ __device__ __forceinline__ void gemv_pipe_body(
     if constexpr (XM == 2) {
       static_assert(XT == BF16X_BF16, "the RMSNorm staging takes bf16 x");
       const int64_t a = min((int64_t)slot, P - 1);
-      load_x_atom<XT>(x, a, xs_reg[i]);                    // h, pair order
-      load_x_atom<XT>(na.w, a, wn_reg[i]);
+      if (slot < G * APW) {                                // h and w raw (natural order)
+        load_x_raw(x, a, xs_reg[i]);
+        load_x_raw(na.w, a, wn_reg[i]);
+      } else {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) xs_reg[i][k] = wn_reg[i][k] = 0u;
+      }
     } else if constexpr (XM == 1) {
       static_assert(XT == BF16X_BF16, "the RMSNorm staging takes bf16 x");
       const int64_t a = min((int64_t)slot, P - 1);
@@ -389,11 +423,15 @@ __device__ __forceinline__ void gemv_pipe_body(
       }
     } else if constexpr (PRE::active) {
       load_x_atom_coherent(rx, min((int64_t)slot, P - 1), xs_reg[i]);
+    } else if constexpr (XT == BF16X_BF16) {
+      if (slot < G * APW) load_x_raw(x, min((int64_t)slot, P - 1), xs_reg[i]);  // slot index = atom index
     } else {
-      load_x_atom<XT>(x, min((int64_t)slot, P - 1), xs_reg[i]);  // slot index = atom index
+      load_x_atom<XT>(x, min((int64_t)slot, P - 1), xs_reg[i]);
     }
   }
   if constexpr (!PRE::active) load_row(r, bufA);
+  // the entries' addresses wait for the offsets: not before the atom loads
+  __builtin_amdgcn_sched_barrier(0);
   // the first row's entries go out before the staging waits (XM = 1 waits for
   // its loads and a barrier before the x stores)
   if constexpr (EXACT && XM != 0) load_ents(eb, ee, entA, satA);
@@ -426,6 +464,7 @@ __device__ __forceinline__ void gemv_pipe_body(
   for (int i = 0; i < XSLOTS; ++i) {
     const int slot = tid + 256 * i;
     if (slot < G * APW) {
+      if constexpr (XM == 2 || (XM == 0 && !PRE::active && XT == BF16X_BF16)) to_pair_order(xs_reg[i]);
       u32x4* dst = (u32x4*)lds + (int64_t)((slot >> 6) * NC) * 64 + (slot & 63);
 #pragma unroll
       for (int c = 0; c < NC; ++c)
