@@ -62,8 +62,11 @@ __global__ __launch_bounds__(256) void gemv_pipe_kernel(
 // would make the compiler keep the whole pass schedule's registers live).
 constexpr int kLongMaxIters = 16;
 
+// Rows of up to 7 passes are held to 128 VGPRs (4 waves per SIMD, the
+// occupancy the launch shapes assume; the prologue's raw x took some
+// variants just past it).
 template <int NP, int XS, bool EXACT, bool FULL, int RES = 0>
-__global__ __launch_bounds__(256) void gemv_long_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(NP <= 7 ? 4 : 1))) void gemv_long_kernel(
     const uint16_t* __restrict__ x, const uint32_t* __restrict__ sign, const uint32_t* __restrict__ mant,
     const uint32_t* __restrict__ delta, const uint16_t* __restrict__ emax2,
     const uint32_t* __restrict__ tile_off, const uint32_t* __restrict__ tile_ent,
@@ -118,30 +121,47 @@ __global__ __launch_bounds__(256) void gemv_long_kernel(
   };
 
   // prologue, in the order the data is needed: offsets of rows 0 and 1, x
-  // (registers), the first two passes, the entries of row 0; x to LDS
+  // (raw words, registers), the first two passes; x to LDS in pair order,
+  // waiting for x alone; the entries of row 0 (their addresses wait for the
+  // offsets, so they go out after the passes)
   uint32_t ob0 = 0, ob1 = 0, on0 = 0, on1 = 0;
   if constexpr (EXACT) {
     load_off(0, ob0, ob1);
     load_off(1, on0, on1);
   }
+  // (RES = 1 keeps x in pair order from its loads, which the compiler then
+  // issues after the passes: the raw x registers live across the passes
+  // took that variant past 128 VGPRs, i.e. from 4 to 3 waves per SIMD)
+  constexpr bool kRawX = RES == 0;
   uint32_t xs[XS][16];
 #pragma unroll
-  for (int i = 0; i < XS; ++i) load_x_atom<BF16X_BF16>(x, min((int64_t)(threadIdx.x + 256 * i), P - 1), xs[i]);
+  for (int i = 0; i < XS; ++i) {
+    const int64_t a = min((int64_t)(threadIdx.x + 256 * i), P - 1);
+    if constexpr (kRawX) {
+      if (threadIdx.x + 256 * i < NP * 64) load_x_raw(x, a, xs[i]);
+    } else {
+      load_x_atom<BF16X_BF16>(x, a, xs[i]);
+    }
+  }
   Atom R[2];
   load_pass(0, 0, R[0]);
   load_pass(0, 1, R[1]);
+  __builtin_amdgcn_sched_barrier(0);
   uint32_t ent[NB] = {};
   uint8_t sat[NB] = {};
-  if constexpr (EXACT) load_ents(ob0, ob1, ent, sat);
+  if constexpr (EXACT && !kRawX) load_ents(ob0, ob1, ent, sat);
 #pragma unroll
   for (int i = 0; i < XS; ++i) {
     const int a = threadIdx.x + 256 * i;
     if (a < NP * 64) {
+      if constexpr (kRawX) to_pair_order(xs[i]);
       u32x4* dst = (u32x4*)lds + (a >> 6) * 4 * 64 + (a & 63);
 #pragma unroll
       for (int c = 0; c < 4; ++c) dst[c * 64] = u32x4{xs[i][4 * c], xs[i][4 * c + 1], xs[i][4 * c + 2], xs[i][4 * c + 3]};
     }
   }
+  // raw x: the entries after the x stores, when its registers are free
+  if constexpr (EXACT && kRawX) load_ents(ob0, ob1, ent, sat);
   __syncthreads();
 
   const u32x4* xl = (const u32x4*)lds + lane;

@@ -297,8 +297,11 @@ __global__ __launch_bounds__(256) void gguf_gemv_long_kernel(const uint8_t* __re
     return (bf16lo_to_f32(bits) - bf16lo_to_f32(bits & 0x807Fu)) * x_at(col);
   };
 
-  // prologue: offsets of rows 0 and 1, paired x (registers), the first two
-  // passes, the entries of row 0; x to LDS
+  // prologue: offsets of rows 0 and 1, x (registers, natural order, by the
+  // threads that store it: loads under the store's condition stay ahead of
+  // the passes instead of being moved behind them), the first two passes,
+  // the entries of row 0 (their addresses wait for the offsets); x to LDS in
+  // pair order, waiting for x alone
   uint32_t ob0 = 0, ob1 = 0, on0 = 0, on1 = 0;
   if constexpr (OVF) {
     load_off(0, ob0, ob1);
@@ -308,13 +311,16 @@ __global__ __launch_bounds__(256) void gguf_gemv_long_kernel(const uint8_t* __re
   u32x4 xs[XS][4];                              // block a's 32 x values, natural order
 #pragma unroll
   for (int i = 0; i < XS; ++i) {
-    const uint32_t a = (uint32_t)min((int64_t)(threadIdx.x + 256 * i), P - 1);
+    if (threadIdx.x + 256 * i < NP * 64) {
+      const uint32_t a = (uint32_t)min((int64_t)(threadIdx.x + 256 * i), P - 1);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) xs[i][q] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(a * 64 + 16 * q), 0, 0);
+      for (int q = 0; q < 4; ++q) xs[i][q] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(a * 64 + 16 * q), 0, 0);
+    }
   }
   GgufRaw R[2];
   load_pass(0, 0, R[0]);
   load_pass(0, 1, R[1]);
+  __builtin_amdgcn_sched_barrier(0);
   uint32_t ent[NB] = {};
   if constexpr (OVF) load_ents(ob0, ob1, ent);
 #pragma unroll
