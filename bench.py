@@ -105,10 +105,13 @@ def time_launches(fn, n_launch: int, warmup: int, stream, queued: bool = False) 
 
 def gemm_kernel_name(M: int, out_f: int, in_f: int) -> str:
     """The kernel the fused GEMM path runs for M rows (bfloat16x_amd.bf16x_gemm's
-    default dispatch: bf16x_gemm_rows, else bf16x_gemm in the C ABI)."""
+    default dispatch: bf16x_gemm_rows, bf16x_gemm_chunks, else bf16x_gemm in
+    the C ABI)."""
     from bfloat16x_amd import ops
     if M <= ops.GEMM_ROWS_MAX and in_f in ops.GEMM_ROWS_IN_F:
         return "gemm_rows_kernel (rows streamed as in the GEMV, 16x16x32 MFMA)"
+    if ops._use_chunks(M, out_f, in_f, torch.device("cuda:0")):
+        return "gemm_chunks_kernel (rows streamed in column chunks, 16x16x32 MFMA)"
     if M <= 64 and in_f % 128 == 0:
         return "gemm_skinny2_kernel (16x16x32 MFMA, few rows)"
     if M <= 32:
@@ -255,6 +258,7 @@ def bench_sweep(bx, dev, stream) -> dict:
         if (out_f, in_f) != (1024, 4096):
             for _, p in cps:
                 p.kplan()
+                p.cplan()
             for M in (16, 64, 256, 512, 2048):
                 xm = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16).to(dev)
                 flops = 2.0 * M * out_f * in_f
@@ -375,6 +379,7 @@ def bench_gemm_case(bx, dev, stream, case: str, reps: int, path: str = "fused") 
                                     tile_sat=plan.tile_sat.clone())) for _ in range(nc)]
         for _, p in cps:
             p.kplan()
+            p.cplan()
 
         def fn(i):
             g, p = cps[i % nc]
@@ -649,7 +654,8 @@ def main():
     del dec_out
     gemm_rec = []
     for _, p in copies:
-        p.kplan()                      # step-major plans built once, outside the timed region
+        p.kplan()                      # step-major and chunk plans built once, outside the timed region
+        p.cplan()
     for M in args.gemm_rows:
         xm = torch.randn(M, in_f, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16).to(dev)
         flops = 2.0 * M * out_f * in_f

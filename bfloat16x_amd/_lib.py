@@ -49,6 +49,10 @@ PROTOTYPES = {
                                   _c_i64, _c_i64, _c_i32, _c_i32, _P, _c_i32, _P, _c_i64, _P]),
     "bf16x_gemm_rows": (ctypes.c_int, [_P, _c_i32, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P,
                                        _P, _c_i64, _c_i64, _c_i32, _c_i32, _P, _c_i32, _P]),
+    "bf16x_cplan_size": (_c_i64, [_c_i64, _c_i64]),
+    "bf16x_cplan_build": (ctypes.c_int, [_P, _P, _c_i64, _c_i64, _P, _P, _P]),
+    "bf16x_gemm_chunks": (ctypes.c_int, [_P, _c_i32, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P, _c_i64, _P,
+                                         _P, _c_i64, _c_i64, _c_i32, _c_i32, _P, _c_i32, _P]),
     "bf16x_fp32_to_bf16_host": (ctypes.c_int, [_P, _c_i64, _P, _c_i32]),
     "bf16x_gguf_quantize_host": (ctypes.c_int, [_P, _c_i64, _P, _c_i32]),
     "bf16x_gguf_decode": (ctypes.c_int, [_P, _c_i64, _c_i64, _c_i64, _P, _c_i32, _P]),
@@ -101,7 +105,7 @@ TUNE_KEYS = {
     "gemm_skinny2_max": 0, "gemm_skinny_max": 1, "gemm_bm": 2, "gemm_split": 3, "gemm_ws_min_rows": 4,
     "gemm_ws_split": 5, "skinny_waves": 6, "skinny2_kq": 7, "skinny2_split": 8, "gemv_iters": 9, "gemv_g": 10,
     "gemv_long": 11, "gemv_xm_slots": 12, "gguf_long": 13, "gguf_iters": 14, "attn_split": 15,
-    "gemm_ws_grouped": 16, "gemm_ws_resident": 17, "attn_mfma": 18,
+    "gemm_ws_grouped": 16, "gemm_ws_resident": 17, "attn_mfma": 18, "chunk_atoms": 19,
 }
 
 _LIB = None

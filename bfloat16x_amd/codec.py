@@ -115,7 +115,8 @@ class Bf16xPlan:
     """Device overflow plan: tile_off uint32 [n_tiles+1], tile_ent uint32 [n_fix]
     ((column << 16) | exact bits), tile_sat uint8 [n_fix] (max(emax - 7, 0)).
     kp_off / kp_ent: the step-major regrouping used by the GEMM, built on the
-    device on first use (see kplan())."""
+    device on first use (see kplan()); cp_off / cp_ent: the chunk plan of the
+    few-row GEMM (see cplan())."""
     tile_off: torch.Tensor
     tile_ent: torch.Tensor
     tile_sat: torch.Tensor
@@ -124,12 +125,16 @@ class Bf16xPlan:
     in_f: int
     kp_off: torch.Tensor | None = None
     kp_ent: torch.Tensor | None = None
+    cp_off: torch.Tensor | None = None
+    cp_ent: torch.Tensor | None = None
 
     @property
     def nbytes(self) -> int:
         n = self.tile_off.numel() * 4 + self.tile_ent.numel() * 4 + self.tile_sat.numel()
         if self.kp_off is not None:
             n += self.kp_off.numel() * 4 + self.kp_ent.numel() * 4
+        if self.cp_off is not None:
+            n += self.cp_off.numel() * 4 + self.cp_ent.numel() * 4
         return n
 
     def kplan(self):
@@ -146,6 +151,25 @@ class Bf16xPlan:
             _lib.check(st, "bf16x_kplan_build")
             self.kp_off, self.kp_ent = kp_off, kp_ent
         return self.kp_off, self.kp_ent
+
+    def cplan(self):
+        """(cp_off, cp_ent) on the plan's device, built once by
+        bf16x_cplan_build: the entries regrouped by (256-column chunk, row)
+        for the chunked few-row GEMM."""
+        if self.cp_off is None:
+            dev = self.tile_off.device
+            if not self.tile_off.is_cuda:
+                raise ValueError("cplan(): the plan must live on the GPU")
+            size = int(_lib.lib().bf16x_cplan_size(self.out_f, self.in_f))
+            if size < 0:
+                raise _lib.Bf16xError(size, "bf16x_cplan_size")
+            cp_off = torch.empty(size, dtype=torch.int32, device=dev)
+            cp_ent = torch.zeros(self.n_fix + 1, dtype=torch.int32, device=dev)
+            st = _lib.lib().bf16x_cplan_build(self.tile_off.data_ptr(), self.tile_ent.data_ptr(), self.out_f,
+                                              self.in_f, cp_off.data_ptr(), cp_ent.data_ptr(), _lib.stream_of(dev))
+            _lib.check(st, "bf16x_cplan_build")
+            self.cp_off, self.cp_ent = cp_off, cp_ent
+        return self.cp_off, self.cp_ent
 
     def to(self, device) -> "Bf16xPlan":
         return Bf16xPlan(self.tile_off.to(device), self.tile_ent.to(device), self.tile_sat.to(device),

@@ -440,6 +440,11 @@ __global__ __launch_bounds__(1024) void kplan_scan_kernel(uint32_t* __restrict__
   if (t == 1023) a[n] = part[1023];
 }
 
+// Exclusive scan of a[0..n) in place on `st`, a[n] = the total (one block).
+void scan_offsets(uint32_t* a, int64_t n, hipStream_t st) {
+  hipLaunchKernelGGL(kplan_scan_kernel, dim3(1), dim3(1024), 0, st, a, n);
+}
+
 }  // namespace bf16x
 
 using namespace bf16x;
@@ -460,7 +465,7 @@ int kplan_build(const uint32_t* tile_off, const uint32_t* tile_ent, int64_t out_
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL((kplan_pass_kernel<false, GE>), dim3((unsigned)G), dim3(64), 0, st, tile_off, tile_ent, out_f,
                      (int)S, (int)G2, kp_off, kp_ent);
-  hipLaunchKernelGGL(kplan_scan_kernel, dim3(1), dim3(1024), 0, st, kp_off, S * G2);
+  scan_offsets(kp_off, S * G2, st);
   hipLaunchKernelGGL((kplan_pass_kernel<true, GE>), dim3((unsigned)G), dim3(64), 0, st, tile_off, tile_ent, out_f,
                      (int)S, (int)G2, kp_off, kp_ent);
   return launch_status();

@@ -10,6 +10,11 @@
 // Kernel-choice override of bf16x_set_tuning (abi_info.cpp): -1 = automatic.
 int64_t bf16x_tuning_value(int key);
 
+namespace bf16x {
+// Exclusive scan of a[0..n) in place on `st`, a[n] = the total (gemm.hip).
+void scan_offsets(uint32_t* a, int64_t n, hipStream_t st);
+}  // namespace bf16x
+
 namespace {
 
 inline int64_t tuning(int key) { return bf16x_tuning_value(key); }

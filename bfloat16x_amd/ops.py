@@ -311,6 +311,27 @@ def bf16x_fused_gemv(x, sign, mant, delta, emax, olk, old, oloff, out_f, in_f, g
 # kernel (bf16x_gemm_rows in the C ABI: weights of 2048 or 4096 columns).
 GEMM_ROWS_MAX = 16
 GEMM_ROWS_IN_F = (2048, 4096)
+# Activation rows for which bf16x_gemm runs the chunked few-row kernel
+# (bf16x_gemm_chunks: in_f % 256 == 0), for weights of at most
+# GEMM_CHUNKS_MAX_IN_F columns, except above 32 rows when a CU has 16 rows or
+# fewer (each CU then reads more x than weight).  Measured, exact, weights
+# rotated through HBM, chunked against the 16x16x32 few-row kernel (us):
+# 14336x4096 M = 24 / 32 / 48 / 64: 29.0 / 30.2 / 36.8 / 38.7 against 32.0 /
+# 32.0 / 43.0 / 44.3; 4096x4096 M = 24 / 32: 16.4 / 17.5 against 19.9 / 19.6,
+# M = 64: 22.6 against 20.8; 4096x14336 M = 32: 44.9 against 33.8.
+GEMM_CHUNKS_MIN = 17
+GEMM_CHUNKS_MAX = 64
+GEMM_CHUNKS_MAX_IN_F = 8192
+
+
+def _cus(dev) -> int:
+    return torch.cuda.get_device_properties(dev).multi_processor_count
+
+
+def _use_chunks(M: int, out_f: int, in_f: int, dev) -> bool:
+    if not (GEMM_CHUNKS_MIN <= M <= GEMM_CHUNKS_MAX) or in_f % 256 or in_f > GEMM_CHUNKS_MAX_IN_F:
+        return False
+    return M <= 32 or -(-out_f // _cus(dev)) > 16
 # One bf16 activation row goes to the GEMV (bf16x_gemv), which streams the
 # weight faster than any GEMM kernel at one row (14336x4096: 19.4 against
 # 24.2 us for the row-streaming GEMM).
@@ -320,18 +341,27 @@ GEMM_ONE_ROW_GEMV = True
 def _gemm_launch(x2, s, m, d, e, out_f, in_f, plan, y, y_dtype, sub=16):
     mode = _lib.SATURATED if plan is None else _lib.EXACT
     L = _lib.lib()
-    if x2.shape[0] <= GEMM_ROWS_MAX and in_f in GEMM_ROWS_IN_F:
-        st = L.bf16x_gemm_rows(x2.data_ptr(), _lib.BF16, x2.shape[0], s.data_ptr(), s.numel(), m.data_ptr(),
+    M = x2.shape[0]
+    if M <= GEMM_ROWS_MAX and in_f in GEMM_ROWS_IN_F:
+        st = L.bf16x_gemm_rows(x2.data_ptr(), _lib.BF16, M, s.data_ptr(), s.numel(), m.data_ptr(),
                                m.numel(), d.data_ptr(), d.numel(), e.data_ptr(), e.numel(),
                                _lib.ptr(plan.tile_off) if plan is not None else None,
                                _lib.ptr(plan.tile_ent) if plan is not None else None, out_f, in_f, int(sub),
                                mode, y.data_ptr(), y_dtype, _lib.stream_of(s.device))
         _lib.check(st, "bf16x_gemm_rows")
         return
+    if _use_chunks(M, out_f, in_f, x2.device):
+        cp_off, cp_ent = plan.cplan() if plan is not None else (None, None)
+        st = L.bf16x_gemm_chunks(x2.data_ptr(), _lib.BF16, M, s.data_ptr(), s.numel(), m.data_ptr(),
+                                 m.numel(), d.data_ptr(), d.numel(), e.data_ptr(), e.numel(), _lib.ptr(cp_off),
+                                 _lib.ptr(cp_ent), out_f, in_f, int(sub), mode, y.data_ptr(), y_dtype,
+                                 _lib.stream_of(s.device))
+        _lib.check(st, "bf16x_gemm_chunks")
+        return
     kp_off, kp_ent = plan.kplan() if plan is not None else (None, None)
-    ws_bytes = int(L.bf16x_gemm_workspace(x2.shape[0], out_f, in_f))
+    ws_bytes = int(L.bf16x_gemm_workspace(M, out_f, in_f))
     ws = torch.empty((ws_bytes + 3) // 4, dtype=torch.float32, device=x2.device) if ws_bytes else None
-    st = L.bf16x_gemm(x2.data_ptr(), _lib.BF16, x2.shape[0], s.data_ptr(), s.numel(), m.data_ptr(),
+    st = L.bf16x_gemm(x2.data_ptr(), _lib.BF16, M, s.data_ptr(), s.numel(), m.data_ptr(),
                       m.numel(), d.data_ptr(), d.numel(), e.data_ptr(), e.numel(), _lib.ptr(kp_off),
                       _lib.ptr(kp_ent), out_f, in_f, int(sub), mode, y.data_ptr(), y_dtype,
                       _lib.ptr(ws), ws_bytes, _lib.stream_of(s.device))
@@ -368,8 +398,9 @@ def bf16x_gemm(x, sign, mant, delta, emax, out_f, in_f, plan: Bf16xPlan | None =
     saturated without one.
 
     path "fused": the fused decode+GEMM kernels (bf16x_gemm_rows up to
-    GEMM_ROWS_MAX rows at in_f 2048 / 4096, else bf16x_gemm in the C ABI; one
-    bf16 row the fused GEMV, bf16x_gemv);
+    GEMM_ROWS_MAX rows at in_f 2048 / 4096, bf16x_gemm_chunks from
+    GEMM_CHUNKS_MIN to GEMM_CHUNKS_MAX rows (see _use_chunks), else
+    bf16x_gemm in the C ABI; one bf16 row the fused GEMV, bf16x_gemv);
     bf16 activations run one bf16 MFMA pass, fp16/fp32 activations are split
     as x = hi + lo (two bf16 tensors, exact for fp16, 16 mantissa bits for
     fp32) accumulated over two passes in fp32.

@@ -217,6 +217,43 @@ int bf16x_gemm_rows(const void* x, int32_t x_dtype, int64_t M,
                     int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
                     void* y, int32_t y_dtype, bf16x_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Chunk plan for bf16x_gemm_chunks (no reference counterpart: the reference
+ * GEMM has no overflow correction, bf16x_gemm_fused.py:9-12).  Built on the
+ * device from the row plan (tile_off / tile_ent of bf16x_plan_host or
+ * bf16x_plan_from_csr; a row's entries sorted by column, as every plan
+ * builder here writes them): the entries regrouped by (256-column chunk p,
+ * row r), so that those of rows [r0, r1) in chunk p are the one run
+ * cp_ent[cp_off[p * out_f + r0] .. cp_off[p * out_f + r1]), each entry
+ * (r & 255) << 24 | (column - 256 p) << 16 | exact bf16 bits.
+ * cp_off: uint32 [bf16x_cplan_size(out_f, in_f)] = [out_f * in_f / 256 + 1];
+ * cp_ent: uint32 [n_fix + 1] (the last word is never an entry).  Requires
+ * in_f % 256 == 0 and in_f <= 65536 (bf16x_cplan_size returns BF16X_ESHAPE
+ * otherwise).  All pointers dev.
+ * ------------------------------------------------------------------------ */
+int64_t bf16x_cplan_size(int64_t out_f, int64_t in_f);
+int bf16x_cplan_build(const uint32_t* tile_off, const uint32_t* tile_ent, int64_t out_f, int64_t in_f,
+                      uint32_t* cp_off, uint32_t* cp_ent, bf16x_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused decode + GEMM for up to 64 activation rows, the product of
+ * bf16x_gemm at the reference's small blocks (bf16x_gemm_fused.py:97-114,
+ * BM = 16 .. 64): y[M, out_f] = x[M, in_f] . W^T, fp32 accumulation, for
+ * 1 <= M <= 64, in_f % 256 == 0 and in_f <= 65536.  A workgroup per CU
+ * streams its rows of W in column chunks (each stream read once), decodes a
+ * chunk into LDS once and multiplies it by every token; no workspace.  EXACT
+ * takes the chunk plan (cp_off, cp_ent of bf16x_cplan_build).  x: dev bf16
+ * [M, in_f], 16-byte aligned; y: dev [M, out_f] of y_dtype (BF16X_BF16 or
+ * BF16X_F32), 4-byte aligned.  Other shapes return BF16X_ESHAPE.  All
+ * pointers dev.
+ * ------------------------------------------------------------------------ */
+int bf16x_gemm_chunks(const void* x, int32_t x_dtype, int64_t M,
+                      const int32_t* sign, int64_t n_sign, const int32_t* mant, int64_t n_mant,
+                      const int32_t* delta, int64_t n_delta, const uint8_t* emax, int64_t n_emax,
+                      const uint32_t* cp_off, const uint32_t* cp_ent,
+                      int64_t out_f, int64_t in_f, int32_t sub, int32_t mode,
+                      void* y, int32_t y_dtype, bf16x_stream_t stream);
+
 /* ========================================================================
  * GGUF half-block variant (bf16x_gguf_block.py, GGML_TYPE_BF16X): blocks of
  * 32 row-major weights, 46 bytes = [emax[2] | sign[4] | mant[28] |
@@ -348,7 +385,8 @@ enum {
   BF16X_TUNE_GEMM_WS_GROUPED = 16, /* 0: the wave-specialised GEMM in one-step (64-column) tiles   */
   BF16X_TUNE_GEMM_WS_RESIDENT = 17,/* resident blocks the wave-specialised GEMM plans its rounds for */
   BF16X_TUNE_ATTN_MFMA = 18,       /* prefill attention: 0 the scalar kernel, 1 the MFMA kernel       */
-  BF16X_TUNE_COUNT = 19
+  BF16X_TUNE_CHUNK_ATOMS = 19,     /* atoms per row and chunk of the chunked few-row GEMM (8, 16, 32) */
+  BF16X_TUNE_COUNT = 20
 };
 int bf16x_set_tuning(int32_t key, int64_t value);
 /* Current value of a key (-1 = automatic; also returned for an unknown key). */
