@@ -140,7 +140,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   constexpr int RS = CA * 64 + 16;             // tile row stride, bytes
   constexpr int TILE = ROWS * RS;
   constexpr int PPC = CA * 32 / kPlanCols;     // plan chunks per chunk (entry runs per wave)
-  constexpr int NBR = PPC == 1 ? 2 : 1;        // entry loads (of 64) per run
+  // entry loads (of 64) per run; one at CA = 8 measured 1-2 us slower (the
+  // loop for longer runs then runs in about 1 % of the chunks)
+  constexpr int NBR = PPC == 1 ? 2 : 1;
   constexpr int RED = kWaves * RT * TTW * 64 * 16;
   constexpr int BIG = 2 * TILE > RED ? 2 * TILE : RED;
   static_assert(APL >= 1 && (64 * APL) % CA == 0 && KS >= 1 && CA % WPG == 0, "chunk shape");
