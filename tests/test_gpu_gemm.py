@@ -220,3 +220,27 @@ def test_gemm_ws_mixed_rounds(bx, tune, grouped, resident, M, out_f, in_f):
                               out_f, in_f, plan=p, path="fused")
             assert y.dtype == dt
             check_tol(y.float().cpu().numpy(), dc.gemm_ref(dn, x.float().numpy(), saturated=sat))
+
+
+# Split tiles' fp32 partials are summed in K-range order by the reduction
+# launch: repeated launches give the same bits, fp32 and bf16, and the
+# result is the product to the north-star tolerance.
+@pytest.mark.parametrize("split", [2, 5])
+def test_gemm_ws_split_sum_is_deterministic(bx, tune, split):
+    M, out_f, in_f = 256, 1024, 4096
+    print("gemm ws split determinism", split, flush=True)
+    tune(gemm_ws_split=split)
+    bits = dc.bench_weight_bits(out_f, in_f, seed=split)
+    d = bx.bf16x_quantize(bits_tensor(bits))
+    g = to_dev(d)
+    plan = bx.build_plan_host(d, device=DEV)
+    x = torch.randn(M, in_f, generator=torch.Generator().manual_seed(split)).to(torch.bfloat16).to(DEV)
+    for dt in (torch.float32, torch.bfloat16):
+        xs = x.to(dt)
+        ys = [bx.bf16x_gemm(xs, g["sign_packed"], g["mant_packed"], g["delta_packed"], g["emax"], out_f, in_f,
+                            plan=plan, path="fused") for _ in range(4)]
+        for yk in ys[1:]:
+            assert torch.equal(yk.view(torch.int32 if dt == torch.float32 else torch.int16),
+                               ys[0].view(torch.int32 if dt == torch.float32 else torch.int16))
+    mx, med = dc.rel_err(ys[0].float().cpu().numpy(), dc.gemm_ref(_np(d), x.float().cpu().numpy(), saturated=False))
+    assert mx <= 1e-2 and med <= 2e-3, (mx, med)
