@@ -376,10 +376,15 @@ int launch_gemv(const void* x, const uint32_t* sign, const uint32_t* mant, const
       (out_f + 1) * P * 28 < (int64_t)0xFFFFFFFF)
     return launch_gemv_long(x, sign, mant, delta, emax2, to, te, ts, out_f, in_f, y, st);
   // parts of 64*NS atoms per wave; G = ceil(P / (64*NS)) waves per row.
-  // NS = 2 unless rows are few (then 1, for more waves in flight).
+  // NS = 2, and a row that one wave takes whole (in_f <= 4096) stays whole
+  // at every row count (launches queued on the GPU, one wave per row against
+  // two half rows: 1024x4096 4.15 against 4.50 us, 3072x4096 6.67 against
+  // 7.04, 1024x3072 3.94 against 4.30, 512x4096 3.66 against 3.84); wider
+  // rows split over more waves when rows are few (NS = 1, more waves in
+  // flight).
   int NS = (P > 64) ? 2 : 1;
   int G = (int)((P + 64 * NS - 1) / (64 * NS));
-  if (NS == 2 && out_f * G < 4096 && (P + 63) / 64 <= 4) { NS = 1; G = (int)((P + 63) / 64); }
+  if (NS == 2 && G > 1 && out_f * G < 4096 && (P + 63) / 64 <= 4) { NS = 1; G = (int)((P + 63) / 64); }
   if (G == 3) G = 4;  // the fourth part of each row is empty
   const int g_req = gemv_g_override();
   if (g_req == 1 || g_req == 2 || g_req == 4) {
