@@ -79,9 +79,12 @@ constexpr uint32_t kDead = 0x7FFFFF00u;
 
 __device__ __forceinline__ int tile_chunk(int a, int q) { return (q ^ (a >> 2)) & 3; }
 
-// The words of one atom as loaded.
+// The words of one atom as loaded (e kept 16-bit, as Atom::e: a 32-bit e is
+// a widened copy of the load, which the compiler places at the loop latch,
+// where it waits for every load in flight: the chunks requested ahead).
 struct Raw {
-  uint32_t s, m[7], d[3], e;
+  uint32_t s, m[7], d[3];
+  uint16_t e;
 };
 
 // Per-lane byte offsets of one atom slot in the four streams (the atom's
